@@ -1,0 +1,194 @@
+#!/usr/bin/env python3
+"""Benchmark of the MXFP4 A4W4 GEMM on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+
+Headline workload: C[8192,8192] bf16 =
+dequant(A)·dequant(B)^T with M=N=K=8192, operands drawn by the seeded
+generator (A ~ N(0,1) with 1% of K-channels x20, W ~ N(0,0.02)), quantized
+to MXFP4 and preshuffled on the GPU by this package, resident in HBM before
+timing.  A step is one call of the drop-in operator mbs_gemm_a4w4.gemm_a4w4.
+
+Also reported (same JSON line): the decode shapes of configs[2]
+(M in {1,4,16,32}, N=K=8192) measured cold -- ten rotating weight copies,
+more than the 256 MB MALL -- replayed from a HIP graph; and the CPU baseline
+(the oracle's restatement of the reference's run_torch on this host's cores,
+on a bounded sample).
+
+One GPU only: --gpus above 1 exits with an explanation.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MXFP4 GEMM TFLOPS & % FP4 MFMA peak (M=N=K=8192); decode HBM GB/s (M=1–16)"
+PEAK_FP4_TFLOPS = 10100.0      # MI355X dense MXFP4 MFMA
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+
+
+def algo_bytes(M, N, K):
+    return M * K // 2 + N * K // 2 + (M + N) * K // 32 + 2 * M * N
+
+
+def prepare(M, N, K, cfg, dev):
+    """Seeded bf16 operands -> MXFP4 bytes on the GPU (product kernels)."""
+    import mbs_amd
+    from mbs_amd import synthetic
+
+    x, w = synthetic.make_operands(cfg, M, N, K)
+    xd, wd = x.to(dev), w.to(dev)
+    A, As = mbs_amd.quantize_mxfp4(xd, shuffle=True)
+    Wp, Bs = mbs_amd.quantize_mxfp4(wd, shuffle=True)
+    B = mbs_amd.shuffle_weight(Wp)
+    del xd, wd, Wp
+    return (A, B, As, Bs), (x, w)
+
+
+def time_steps(fn, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(s)
+    for _ in range(steps):
+        fn()
+    e1.record(s)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_time(e1) / 1e3, wall   # seconds (events), seconds (host clock)
+
+
+def decode_bench(dev, Ms=(1, 4, 16, 32), N=8192, K=8192, copies=10, replays=20):
+    """Cold (rotating copies) and warm per-launch time of the decode shapes,
+    from HIP-graph replay so host launch overhead is excluded."""
+    import torch
+
+    import mbs_amd
+
+    (_, B, _, Bs), _ = prepare(32, N, K, 2, dev)
+    Bc = [B.clone() for _ in range(copies)]
+    Bsc = [Bs.clone() for _ in range(copies)]
+    del B, Bs
+    res = {}
+    for M in Ms:
+        (A, _, As, _), _ = prepare(M, 16, K, 2, dev)
+        for mode in ("cold", "warm"):
+            idx = list(range(copies)) if mode == "cold" else [0] * copies
+            run = lambda: [mbs_amd.gemm_a4w4(A, Bc[i], As, Bsc[i]) for i in idx]
+            run()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                run()
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(replays):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (replays * copies)
+            gbs = algo_bytes(M, N, K) / (us * 1e-6) / 1e9
+            res.setdefault(f"M={M}", {})[mode] = {
+                "us": round(us, 3), "GBps": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+            del g
+        res[f"M={M}"]["plan"] = mbs_amd.ext().plan_name(M, N, K)
+    return res
+
+
+def cpu_baseline(x, w, rows=2048, reps=3):
+    """The oracle's run_torch restatement (dequant to fp32, torch.mm fp32,
+    bf16) on this host: `rows` rows of the config-1 A against the full W."""
+    import torch
+
+    import oracle  # the CPU checker; timed here as the reported baseline
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    xp, xs = oracle.quantize_mxfp4(x[:rows].float().numpy())
+    wp, ws = oracle.quantize_mxfp4(w.float().numpy())
+    N, K = w.shape
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        oracle.run_torch(xp, wp, xs, ws)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {
+        "value": round(2.0 * rows * N * K / t / 1e12, 4), "unit": "TFLOPS", "cores": cores,
+        "kind": "port",
+        "sample": f"config-1 rows 0..{rows - 1} of A x full W ({rows}x{N}x{K}): dequant + fp32 "
+                  f"torch.mm + bf16, median of {reps} ({t:.2f} s each)",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode shapes")
+    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures a single MI355X; the MXFP4 GEMM is a one-GPU "
+              "kernel here (multi-GPU sharding is described in DESIGN.md, not run). "
+              "Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import mbs_amd
+
+    dev = torch.device("cuda:0")
+    M = N = K = 8192
+    (A, B, As, Bs), (x, w) = prepare(M, N, K, 1, dev)
+    step = lambda: mbs_amd.gemm_a4w4(A, B, As, Bs)
+    t_ev, t_wall = time_steps(step, args.steps, args.warmup)
+    t_step = max(t_ev, t_wall)
+    flops = 2.0 * M * N * K
+    tflops = flops * args.steps / t_step / 1e12
+    kern_us = t_ev / args.steps * 1e6
+    achieved = flops / (kern_us * 1e-6) / 1e12
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_cfg1.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    line = {
+        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOPS", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(t_step / args.steps * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "mxfp4",
+        "data": "synthetic (seeded; BASELINE configs[1] distributions, quantized on-GPU)",
+        "config": {"workload": "configs[1]: MXFP4 A4W4 GEMM M=N=K=8192, bf16 out",
+                   "M": M, "N": N, "K": K, "plan": mbs_amd.ext().plan_name(M, N, K)},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP4_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP4_TFLOPS, 4),
+                     "traffic": traffic, "kernel_us": round(kern_us, 2),
+                     "algorithmic_bytes": algo_bytes(M, N, K)},
+    }
+    if not args.no_decode:
+        line["decode"] = decode_bench(dev)
+    del A, B, As, Bs
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(x, w)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

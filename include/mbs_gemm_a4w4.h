@@ -1,0 +1,127 @@
+/*
+ * mbs_gemm_a4w4.h -- C ABI of the MI355X (gfx950) MXFP4 A4W4 GEMM library
+ * (libmbs_gemm_kernel.so).  Plain pointers and sizes only; no torch, no HIP
+ * types (streams are passed as void* holding a hipStream_t).
+ *
+ * Data contract (same bytes the reference kernel consumes, see
+ * kernel/gemm_a4w4.h:5-26 of the reference):
+ *   A        [M, K/2]   u8, two e2m1 codes per byte, low nibble = even k,
+ *                       plain row-major.
+ *   B        [N, K/2]   u8, e2m1 pairs, preshuffled with layout (16,16):
+ *                       byte (n,kp) lives at
+ *                       (n/16)*(K*8) + (kp/32)*512 + ((kp%32)/16)*256
+ *                       + (n%16)*16 + kp%16.
+ *   AScale   E8M0 u8, shuffled, >= round_up(M,32)*scaleN_pad bytes:
+ *   BScale   E8M0 u8, shuffled, >= round_up(N,32)*scaleN_pad bytes;
+ *                       byte (r,b) lives at
+ *                       (r/32)*32*scaleN_pad + (b/8)*256 + (b%4)*64
+ *                       + (r%16)*4 + ((b%8)/4)*2 + (r%32)/16.
+ *   AFactor  [M] u8 or NULL, BFactor [N] u8 or NULL (both or neither):
+ *                       out[m][n] *= f(AFactor[m]) * f(BFactor[n]),
+ *                       f(b) = 1/(1+b/256).
+ *   out      [Mpad, N]  bf16, Mpad = round_up(M,32); rows >= M untouched.
+ *   scaleN_pad = round_up(ceil(K/32), 8).
+ * Requirements: M >= 1, N % 16 == 0, K % 64 == 0 (the (16,16) preshuffle
+ * needs K/2 % 32 == 0), all pointers device-accessible.
+ *
+ * Every launch is asynchronous on `stream`; results are deterministic
+ * (split-K partials are reduced in a fixed order, no atomics).
+ */
+#ifndef MBS_GEMM_A4W4_H_
+#define MBS_GEMM_A4W4_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes returned by every entry point. */
+enum {
+    MBS_OK = 0,
+    MBS_ERR_ARGUMENT = 1,  /* null pointer, bad shape or padding argument   */
+    MBS_ERR_WORKSPACE = 2, /* forced config needs more workspace than given */
+    MBS_ERR_LAUNCH = 3,    /* the HIP launch itself failed                  */
+    MBS_ERR_CONFIG = 4     /* forced config id out of range / unusable      */
+};
+
+/* Human-readable text for a status code (static storage). */
+const char* mbs_status_string(int status);
+
+/* Text of the last error raised on the calling thread ("" if none). */
+const char* mbs_last_error(void);
+
+/* MXFP4 A4W4 GEMM.  Replaces gemm_a4w4_mxfp4_launch
+ * (reference kernel/gemm_a4w4.h:27-39, kernel/gemm_a4w4.hip:1044-1146) with
+ * the same argument order, plus a caller-owned workspace for split-K partials
+ * (`workspace` may be NULL when `workspace_bytes` is 0; size it with
+ * mbs_gemm_a4w4_workspace_bytes).  Unlike the reference (which returns false
+ * when factors meet its single-wave kernel) every shape accepts factors.
+ * Returns MBS_OK or an error code; on error nothing is launched. */
+int mbs_gemm_a4w4_launch(const uint8_t* A, const uint8_t* B, const uint8_t* AScale,
+                         const uint8_t* BScale, const uint8_t* AFactor,
+                         const uint8_t* BFactor, void* out, int M, int N, int K, int Mpad,
+                         int scaleN_pad, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/* Workspace the heuristic launch of (M,N,K) wants (0 if it needs none).
+ * Passing less makes mbs_gemm_a4w4_launch fall back to a no-split plan.
+ * No counterpart in the reference (its launcher never splits K). */
+size_t mbs_gemm_a4w4_workspace_bytes(int M, int N, int K);
+
+/* Plan introspection and forced plans, for tests and tuning.  A plan is a
+ * (kernel family, tile, split) triple; mbs_gemm_a4w4_plan_name() describes
+ * the one the heuristic picks for (M,N,K).  mbs_gemm_a4w4_launch_config()
+ * runs kernel configuration `config` (0 <= config < mbs_gemm_a4w4_num_configs())
+ * with `splits` K-splits (0 = the heuristic's choice for that config).
+ * Stands in for the reference's MBS_FORCE_TILE_ENV / MBS_TILE debug switch
+ * (kernel/gemm_a4w4.hip:1094-1102). */
+int mbs_gemm_a4w4_num_configs(void);
+const char* mbs_gemm_a4w4_config_name(int config);
+int mbs_gemm_a4w4_plan_name(int M, int N, int K, char* buf, size_t buf_len);
+size_t mbs_gemm_a4w4_config_workspace_bytes(int config, int splits, int M, int N, int K);
+int mbs_gemm_a4w4_launch_config(int config, int splits, const uint8_t* A, const uint8_t* B,
+                                const uint8_t* AScale, const uint8_t* BScale,
+                                const uint8_t* AFactor, const uint8_t* BFactor, void* out,
+                                int M, int N, int K, int Mpad, int scaleN_pad,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- formats
+ * The on-device format helpers the reference takes from aiter
+ * (test_gemm_a4w4.py:134-141): quantize, preshuffle, dequantize.
+ */
+
+/* bf16 [rows, K] (row stride K) -> packed e2m1 [rows, K/2] + E8M0 scales.
+ * Rule: OCP MX v1.0 MXFP4 -- block exponent floor(log2 amax) - 2 (biased,
+ * clamped to [0,254]; all-zero block -> 0x00), e2m1 round-to-nearest-even,
+ * saturate to +-6, low nibble = even k.  `scale_shuffled` (may be NULL)
+ * receives the shuffled layout of round_up(rows,32)*scaleN_pad bytes with
+ * padding filled with `pad_byte`; `scale_plain` (may be NULL) receives
+ * [rows, K/32].  K % 32 == 0.  Replaces aiter.get_triton_quant(per_1x32)
+ * as called at test_gemm_a4w4.py:134-140 (rounding rule). */
+int mbs_quantize_mxfp4_bf16(const void* x, int rows, int K, uint8_t* packed,
+                            uint8_t* scale_shuffled, uint8_t* scale_plain, int pad_byte,
+                            void* stream);
+
+/* Plain packed weights [N, K/2] -> (16,16)-preshuffled [N, K/2] (out of place).
+ * Replaces aiter.ops.shuffle.shuffle_weight(w, layout=(16,16))
+ * (test_gemm_a4w4.py:141). */
+int mbs_shuffle_b(const uint8_t* w, uint8_t* out, int N, int K, void* stream);
+
+/* Plain E8M0 [rows, K/32] -> shuffled buffer (padding = pad_byte). */
+int mbs_shuffle_scales(const uint8_t* plain, uint8_t* out, int rows, int K, int pad_byte,
+                       void* stream);
+
+/* Packed operand + shuffled scales -> fp32 [rows, K]:
+ * e2m1(code) * 2^(e-127) (e=255 -> NaN).  b_preshuffled selects the B layout
+ * for `packed`.  Replaces fp4_utils.mxfp4_to_f32 * e8m0_to_f32 as used by
+ * run_torch (test_gemm_a4w4.py:33-42); bit-exact by construction. */
+int mbs_dequant_mxfp4(const uint8_t* packed, const uint8_t* scale_shuffled, float* out,
+                      int rows, int K, int b_preshuffled, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MBS_GEMM_A4W4_H_ */

@@ -1,0 +1,95 @@
+"""mbs_amd -- MI355X (gfx950) MXFP4 A4W4 GEMM.
+
+The product is two in-tree shared objects under ``mbs_amd/lib/`` (build them
+with ``python -m mbs_amd._build``):
+
+* ``libmbs_gemm_kernel.so`` -- HIP kernels behind the C ABI declared in
+  ``include/mbs_gemm_a4w4.h``;
+* ``mbs_gemm_a4w4.*.so`` -- the torch module with the reference's operator
+  ``gemm_a4w4(A, B, A_scale, B_scale, A_factor=None, B_factor=None)``.
+
+``import mbs_gemm_a4w4`` works once ``mbs_amd/lib`` is on ``sys.path``
+(importing this package puts it there); the names are re-exported here.
+Nothing here falls back to a CPU path: if the libraries are missing the
+import fails.
+"""
+from __future__ import annotations
+
+import ctypes
+import glob
+import importlib
+import os
+import sys
+
+LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
+KERNEL_LIB_PATH = os.path.join(LIB_DIR, "libmbs_gemm_kernel.so")
+
+_ext = None
+_clib = None
+
+
+def _load_ext():
+    global _ext
+    if _ext is None:
+        if not glob.glob(os.path.join(LIB_DIR, "mbs_gemm_a4w4*.so")):
+            raise ImportError(
+                f"mbs_gemm_a4w4 extension not built in {LIB_DIR}; run `python -m mbs_amd._build`")
+        import torch  # noqa: F401  (the module links against torch)
+
+        if LIB_DIR not in sys.path:
+            sys.path.insert(0, LIB_DIR)
+        _ext = importlib.import_module("mbs_gemm_a4w4")
+    return _ext
+
+
+def ext():
+    """The ``mbs_gemm_a4w4`` extension module."""
+    return _load_ext()
+
+
+def clib() -> ctypes.CDLL:
+    """ctypes handle on ``libmbs_gemm_kernel.so`` (the C ABI)."""
+    global _clib
+    if _clib is None:
+        if not os.path.exists(KERNEL_LIB_PATH):
+            raise ImportError(f"{KERNEL_LIB_PATH} not built; run `python -m mbs_amd._build`")
+        _clib = ctypes.CDLL(KERNEL_LIB_PATH)
+    return _clib
+
+
+def gemm_a4w4(A, B, A_scale, B_scale, A_factor=None, B_factor=None):
+    """out[M,N] bf16 = dequant(A) @ dequant(B)^T [* f(A_factor)[:,None] * f(B_factor)[None,:]].
+
+    Same contract as the reference's ``mbs_gemm_a4w4.gemm_a4w4``
+    (interface/gemm_a4w4_pybind.cpp:19-64): A [M,K/2] fp4x2 row-major, B
+    [N,K/2] fp4x2 preshuffled (16,16), shuffled E8M0 scales, optional u8
+    factors.  Asynchronous on the current stream."""
+    return ext().gemm_a4w4(A, B, A_scale, B_scale, A_factor, B_factor)
+
+
+def quantize_mxfp4(x, shuffle: bool = True, pad_byte: int = 127):
+    """bf16 [R,K] device tensor -> (packed u8 [R,K/2], E8M0 scales);
+    shuffled [round_up(R,32), scaleN_pad] when ``shuffle`` else plain [R,K/32]."""
+    return ext().quantize_mxfp4(x, shuffle, pad_byte)
+
+
+def shuffle_weight(w):
+    """(16,16) preshuffle of packed weights [N,K/2] (out of place)."""
+    return ext().shuffle_weight(w)
+
+
+def shuffle_scales(s, pad_byte: int = 127):
+    return ext().shuffle_scales(s, pad_byte)
+
+
+def dequant_mxfp4(packed, scale, b_preshuffled: bool = False):
+    return ext().dequant_mxfp4(packed, scale, b_preshuffled)
+
+
+def scale_pad(K: int) -> int:
+    """scaleN_pad = round_up(ceil(K/32), 8)."""
+    return ((K + 31) // 32 + 7) // 8 * 8
+
+
+def round_up(x: int, m: int) -> int:
+    return (x + m - 1) // m * m

@@ -1,0 +1,792 @@
+// MXFP4 A4W4 GEMM for MI355X (gfx950):  out[M,N] (bf16) =
+//   (dequant(A) . dequant(B)^T) * f(AFactor)[m] * f(BFactor)[n],  fp32 accumulate.
+//
+// Operand bytes follow the reference's contract (kernel/gemm_a4w4.h:5-26 of
+// the reference): plain row-major A [M,K/2], (16,16)-preshuffled B, shuffled
+// E8M0 scales.  Three kernel families:
+//
+//  * gemm_tiled_kernel  -- workgroup tile BM x BN, 4 (or fewer) waves.  A and
+//    B K-slices of 128 (one MFMA depth) are moved global->LDS by 16-byte
+//    buffer_load ... lds DMA into a 4-deep ring, prefetch distance 3.  The LDS
+//    image of each 16-row x 128-K fragment is exactly the MFMA operand order
+//    (lane L's 16 bytes at L*16), so every LDS read is a linear ds_read_b128
+//    with no bank conflicts.  For A the DMA lane->address map performs the
+//    row-major -> fragment reshuffle on the fly; preshuffled B is already in
+//    fragment order.  Scale dwords for each 256-K group ride the same DMA
+//    stream into a 2-slot ring.  The MFMA is issued with the operands swapped
+//    (B as src0) so each lane owns 4 consecutive n of one output row; the
+//    epilogue applies the MBS factors, packs bf16 (RNE) and stores 8 bytes.
+//  * gemm_skinny_kernel -- decode shapes (M <= 32): each wave streams 16 rows
+//    of B straight into VGPRs with all loads of its K-chunk in flight, waves
+//    of a workgroup split K and reduce through LDS in a fixed order.
+//  * splitk_reduce_kernel -- deterministic fixed-order sum of fp32 split-K
+//    partials plus the same epilogue.
+#include "mxfp4_device.h"
+#include "mbs_gemm_a4w4.h"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+namespace mbs {
+
+namespace {
+thread_local std::string g_last_error;
+}
+void set_last_error(const char* msg) { g_last_error = msg ? msg : ""; }
+
+__constant__ FactorTable kFactors = FactorTable();
+
+__device__ __forceinline__ float factor_of(uint32_t b)
+{
+    return __uint_as_float(kFactors.bits[b & 255]);
+}
+
+struct GemmArgs {
+    const uint8_t* A;
+    const uint8_t* B;
+    const uint8_t* As;
+    const uint8_t* Bs;
+    const uint8_t* Af;  // nullable (both or neither)
+    const uint8_t* Bf;
+    uint16_t* out;      // bf16 [Mpad, N]
+    float* ws;          // split-K partials [splits][M][N] fp32, or null
+    int M, N, K, snp;   // snp = scaleN_pad
+    int tiles_m, tiles_n;
+    int splits, sps;    // K-splits and 128-K stages per split (even)
+};
+
+// ======================================================================
+// Tiled kernel
+// ======================================================================
+template <int BM_, int BN_, int WGM_, int WGN_>
+struct TileShape {
+    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
+    static constexpr int NW = WGM * WGN, NT = 64 * NW;
+    static constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile
+    static constexpr int FM = WM / 16, FN = WN / 16;    // 16x16 fragments per wave
+    static constexpr int AF = BM / 16, BF = BN / 16;    // 1-KiB fragments per stage
+    static constexpr int DA = AF / NW, DB = BF / NW;    // data DMAs per wave per stage
+    static constexpr int SGA = BM / 32, SGB = BN / 32;  // 256-B scale groups per 256 K
+    static constexpr int DS = (SGA + SGB + NW - 1) / NW;  // scale DMAs per wave per group
+    static constexpr int SA = FM / 2, SB = FN / 2;      // scale dwords per wave per group
+    static constexpr int STAGE = (AF + BF) * 1024;
+    static constexpr int SCB = DS * NW * 256;
+    static constexpr int NBUF = 4, PF = 3;
+    static_assert(AF % NW == 0 && BF % NW == 0, "fragments must split evenly over waves");
+    static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
+    static_assert(NBUF * STAGE + 2 * SCB <= 160 * 1024, "LDS budget");
+};
+
+template <class T, bool KTAIL, bool SPLIT>
+__global__ void __launch_bounds__(T::NT) gemm_tiled_kernel(const GemmArgs p)
+{
+    // One __shared__ object per ring slot: the compiler tracks in-flight LDS
+    // DMA per LDS object (alias scopes), so distinct objects let it see that
+    // reading slot s does not wait on the DMA into slot s+1..s+3.
+    __shared__ __attribute__((aligned(1024))) uint8_t sd0[T::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t sd1[T::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t sd2[T::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t sd3[T::STAGE];
+    __shared__ __attribute__((aligned(256))) uint8_t ss0[T::SCB];
+    __shared__ __attribute__((aligned(256))) uint8_t ss1[T::SCB];
+    auto sdata = [&](auto B) __attribute__((always_inline)) -> uint8_t* {
+        constexpr int b = decltype(B)::value;
+        if constexpr (b == 0) return sd0;
+        else if constexpr (b == 1) return sd1;
+        else if constexpr (b == 2) return sd2;
+        else return sd3;
+    };
+    auto sscale = [&](auto S) __attribute__((always_inline)) -> uint8_t* {
+        if constexpr (decltype(S)::value == 0) return ss0;
+        else return ss1;
+    };
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = w / T::WGN, wn = w % T::WGN;
+
+    // ---- tile / split assignment: XCD-aware, grouped along M -----------
+    // Workgroups are dealt round-robin over the 8 XCDs; renumber so that
+    // consecutive logical ids share an XCD (and its L2), then walk tiles in
+    // groups of 8 tile-rows so concurrently running tiles share A and B.
+    int bid = blockIdx.x;
+    const int G = gridDim.x;
+    if ((G & 7) == 0) bid = (bid & 7) * (G >> 3) + (bid >> 3);
+    const int tiles = p.tiles_m * p.tiles_n;
+    const int split = bid / tiles;
+    const int t = bid - split * tiles;
+    constexpr int GROUP = 8;
+    const int grp = t / (GROUP * p.tiles_n);
+    const int first_m = grp * GROUP;
+    const int gsz = min(p.tiles_m - first_m, GROUP);
+    const int tin = t - grp * GROUP * p.tiles_n;
+    const int m0 = (first_m + tin % gsz) * T::BM;
+    const int n0 = (tin / gsz) * T::BN;
+
+    const int K = p.K, Kp = K >> 1;
+    const int S_total = (K + 127) >> 7;
+    const int s_begin = split * p.sps;
+    const int n_st = min(p.sps, S_total - s_begin);
+
+    // ---- buffer resources (tile-based so offsets stay small) -----------
+    const int rows_a = min(T::BM, p.M - m0);
+    const int rows_b = min(T::BN, p.N - n0);
+    const int Mpad = (p.M + 31) & ~31, Npad = (p.N + 31) & ~31;
+    const rsrc_t rA = make_rsrc(p.A + (size_t)m0 * Kp, (uint32_t)(rows_a * Kp));
+    const rsrc_t rB = make_rsrc(p.B + (size_t)(n0 >> 4) * K * 8, (uint32_t)(rows_b * Kp));
+    const rsrc_t rAs = make_rsrc(p.As + (size_t)(m0 >> 5) * 32 * p.snp,
+                                 (uint32_t)(min(T::BM, Mpad - m0) * p.snp));
+    const rsrc_t rBs = make_rsrc(p.Bs + (size_t)(n0 >> 5) * 32 * p.snp,
+                                 (uint32_t)(min(T::BN, Npad - n0) * p.snp));
+
+    // ---- per-lane DMA offsets ------------------------------------------
+    // A fragment f, lane i: row 16f + i%16, K-block i/16 of the stage.
+    // B fragment f, lane i: preshuffled, 16 contiguous bytes at i*16.
+    uint32_t voA[T::DA], voB[T::DB];
+    static_for<T::DA>([&](auto d) {
+        const int fa = w * T::DA + d;
+        voA[d] = (uint32_t)((16 * fa + (lane & 15)) * Kp + (lane >> 4) * 16);
+    });
+    static_for<T::DB>([&](auto d) {
+        const int fb = w * T::DB + d;
+        voB[d] = (uint32_t)(fb * K * 8 + lane * 16);
+    });
+    const bool hi_lane = lane >= 32;  // K-blocks 2,3 of a 128-K stage
+    const uint32_t hi_bit = hi_lane ? kOOB : 0u;
+
+    // ---- DMA items ---------------------------------------------------------
+    // One stage's DMA group: DA fragments of A, DB of B and, on the first
+    // stage of a 256-K group, DS scale groups.  Stages past the split's end
+    // are still issued, with every lane out of range: they write zeros into a
+    // free slot and keep the per-stage VMEM count uniform, which the vmcnt
+    // bookkeeping relies on.  The out-of-range bit is OR-ed in rather than
+    // selected: a select on a wave-uniform condition gets turned into a
+    // branch that would split the pipelined loop body.
+    auto dead_bits = [&](int ls) __attribute__((always_inline)) {
+        const int s = s_begin + ls;
+        uint32_t dead = (uint32_t)(ls >= n_st) << 31;
+        if (KTAIL) dead |= ((uint32_t)(s == S_total - 1) << 31) & hi_bit;
+        asm volatile("" : "+v"(dead));
+        return dead;
+    };
+    auto issue_item = [&](auto BUF, auto D, int ls, uint32_t dead) __attribute__((always_inline)) {
+        constexpr int d = decltype(D)::value;
+        const int s = s_begin + ls;
+        if constexpr (d < T::DA) {
+            dma16(rA, sdata(BUF) + (w * T::DA + d) * 1024, (voA[d] + (uint32_t)s * 64u) | dead);
+        } else if constexpr (d < T::DA + T::DB) {
+            constexpr int e = d - T::DA;
+            dma16(rB, sdata(BUF) + (T::AF + w * T::DB + e) * 1024,
+                  (voB[e] + (uint32_t)s * 1024u) | dead);
+        } else {
+            constexpr int e = d - T::DA - T::DB;
+            constexpr int slot = (decltype(BUF)::value >> 1) & 1;
+            const int q = w * T::DS + e;
+            const bool is_a = q < T::SGA;
+            const bool is_b = !is_a && q < T::SGA + T::SGB;
+            const uint32_t g = (uint32_t)(s >> 1) * 256u + lane * 4;
+            const uint32_t qdead = ((uint32_t)(ls >= n_st) | (uint32_t)!(is_a || is_b)) << 31;
+            const uint32_t base = (uint32_t)((is_a ? q : q - T::SGA) * 32 * p.snp);
+            dma4(is_a ? rAs : rBs, sscale(std::integral_constant<int, slot>{}) + q * 256,
+                 (base + g) | qdead);
+        }
+    };
+    // VMEM ops one wave issues per local stage (static parity).
+    constexpr int CNT_ODD = T::DA + T::DB;
+    constexpr int CNT_EVEN = T::DA + T::DB + T::DS;
+
+    i32x4 ra[2][T::FM], rb[2][T::FN];
+    int sa[2][T::SA], sb[2][T::SB];
+    f32x4 acc[T::FM][T::FN];
+    static_for<T::FM>([&](auto i) {
+        static_for<T::FN>([&](auto j) { acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f}; });
+    });
+
+    // ---- LDS read items: stage in slot BUF -> register set R ----------------
+    auto read_item = [&](auto BUF, auto R, auto X) __attribute__((always_inline)) {
+        constexpr int r = decltype(R)::value;
+        constexpr int x = decltype(X)::value;
+        constexpr int slot = (decltype(BUF)::value >> 1) & 1;
+        if constexpr (x < T::FM) {
+            ra[r][x] = *reinterpret_cast<const i32x4*>(sdata(BUF) + (wm * T::FM + x) * 1024 +
+                                                       lane * 16);
+        } else if constexpr (x < T::FM + T::FN) {
+            constexpr int j = x - T::FM;
+            rb[r][j] = *reinterpret_cast<const i32x4*>(
+                sdata(BUF) + (T::AF + wn * T::FN + j) * 1024 + lane * 16);
+        } else if constexpr (x < T::FM + T::FN + T::SA) {
+            constexpr int i = x - T::FM - T::FN;
+            sa[slot][i] = *reinterpret_cast<const int*>(
+                sscale(std::integral_constant<int, slot>{}) + ((wm * T::WM) / 32 + i) * 256 +
+                lane * 4);
+        } else {
+            constexpr int j = x - T::FM - T::FN - T::SA;
+            sb[slot][j] = *reinterpret_cast<const int*>(
+                sscale(std::integral_constant<int, slot>{}) +
+                (T::SGA + (wn * T::WN) / 32 + j) * 256 + lane * 4);
+        }
+    };
+    auto read_all = [&](auto BUF, auto R) __attribute__((always_inline)) {
+        constexpr int NX = T::FM + T::FN + (((decltype(BUF)::value & 1) == 0) ? T::SA + T::SB : 0);
+        static_for<NX>([&](auto X) { read_item(BUF, R, X); });
+    };
+
+    // ---- one pipelined stage ----------------------------------------------
+    // Compute stage ls (slot u, registers u&1) while issuing the DMA group of
+    // stage ls+3 and the LDS reads of stage ls+1.  The work is cut into FM
+    // chunks (one A-fragment row of FN MFMAs each) and each chunk carries an
+    // even share of the DMAs and LDS reads; sched_barrier(0) between chunks
+    // keeps the compiler from clustering the reads behind the MFMAs.
+    auto stage = [&](auto U, int ls) __attribute__((always_inline)) {
+        constexpr int u = decltype(U)::value;
+        constexpr int r = u & 1, slot = (u >> 1) & 1, h = u & 1;
+        using BUFN = std::integral_constant<int, (u + 1) & 3>;  // slot read now
+        using BUFD = std::integral_constant<int, (u + 3) & 3>;  // slot refilled now
+        using RN = std::integral_constant<int, (u + 1) & 1>;
+        constexpr int NDMA = T::DA + T::DB + ((((u + 3) & 1) == 0) ? T::DS : 0);
+        constexpr int NRD = T::FM + T::FN + ((((u + 1) & 1) == 0) ? T::SA + T::SB : 0);
+        constexpr int NCH = T::FM;
+
+        // stage ls+1 must have landed for every wave; ls+2 may be in flight
+        wait_vmcnt<((u & 1) == 0) ? CNT_EVEN : CNT_ODD>();
+        barrier();
+        __builtin_amdgcn_sched_barrier(0);
+
+        const uint32_t dead = dead_bits(ls + 3);
+        int sav[T::SA], sbv[T::SB];
+        static_for<T::SA>([&](auto i) { sav[i] = sa[slot][i]; });
+        static_for<T::SB>([&](auto j) { sbv[j] = sb[slot][j]; });
+        if constexpr (KTAIL) {
+            // Blocks past K (zeroed data) get a finite scale so 0 * scale
+            // cannot become NaN when the caller's padding bytes are 0xFF.
+            const bool tail = (s_begin + ls == S_total - 1) && hi_lane;
+            static_for<T::SA>([&](auto i) { sav[i] = tail ? 0x7F7F7F7F : sav[i]; });
+            static_for<T::SB>([&](auto j) { sbv[j] = tail ? 0x7F7F7F7F : sbv[j]; });
+        }
+        static_for<NCH>([&](auto C) {
+            constexpr int c = decltype(C)::value;
+            static_for<NDMA>([&](auto D) {
+                if constexpr (D * NCH / NDMA == c) issue_item(BUFD{}, D, ls + 3, dead);
+            });
+            static_for<NRD>([&](auto X) {
+                if constexpr (X * NCH / NRD == c) read_item(BUFN{}, RN{}, X);
+            });
+            static_for<T::FN>([&](auto j) {
+                constexpr int opb = (j & 1) + 2 * h;
+                constexpr int opa = (c & 1) + 2 * h;
+                mfma_fp4<opb, opa>(acc[c][j], rb[r][j], ra[r][c], sbv[j / 2], sav[c / 2]);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+
+    // ---- prologue --------------------------------------------------------
+    static_for<3>([&](auto P) {
+        constexpr int ps = decltype(P)::value;
+        constexpr int nd = T::DA + T::DB + (((ps & 1) == 0) ? T::DS : 0);
+        const uint32_t dead = dead_bits(ps);
+        static_for<nd>([&](auto D) { issue_item(P, D, ps, dead); });
+    });
+    wait_vmcnt<CNT_ODD + CNT_EVEN>();
+    barrier();
+    read_all(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+
+    // ---- main loop: 4 stages per trip, ring slot = stage % 4 ----------
+    // The stage count is padded to a multiple of 4 with all-zero stages
+    // (zero data, zero scale bytes), which add exactly 0 to the sums.
+    const int n_st4 = (n_st + 3) & ~3;
+    for (int ls0 = 0; ls0 < n_st4; ls0 += 4) {
+        static_for<4>([&](auto U) { stage(U, ls0 + decltype(U)::value); });
+    }
+    // The look-ahead DMAs of the last trip are still writing LDS: drain them
+    // before this workgroup's LDS can be handed to another.
+    wait_vmcnt<0>();
+    mfma_drain();
+
+    // ---- epilogue ----------------------------------------------------------
+    // Factors default to 1.0f, and x * (1.0f * 1.0f) == x exactly, so the
+    // no-factor case runs the same branch-free code.
+    const bool has_f = (p.Af != nullptr) && (p.Bf != nullptr);
+    const int row_l = wm * T::WM + (lane & 15);        // row within tile (frag 0)
+    const int col_w = n0 + wn * T::WN;                  // first column of the wave
+    const int colq = (lane >> 4) * 4;                   // lane's 4 columns in a frag
+    if constexpr (SPLIT) {
+        const rsrc_t rW = make_rsrc(p.ws + ((size_t)split * p.M + m0) * p.N,
+                                    (uint32_t)(rows_a * p.N * 4));
+        static_for<T::FN>([&](auto j) {
+            const int c = col_w + j * 16;
+            if (c < p.N) {
+                static_for<T::FM>([&](auto i) {
+                    store16(rW, (uint32_t)(((row_l + i * 16) * p.N + c + colq) * 4), acc[i][j]);
+                });
+            }
+        });
+    } else {
+        const rsrc_t rAf = make_rsrc(p.Af + m0, has_f ? (uint32_t)rows_a : 0u);
+        const rsrc_t rBf = make_rsrc(p.Bf, has_f ? (uint32_t)p.N : 0u);
+        const rsrc_t rO = make_rsrc(p.out + (size_t)m0 * p.N, (uint32_t)(rows_a * p.N * 2));
+        float fa[T::FM];
+        static_for<T::FM>([&](auto i) {
+            fa[i] = has_f ? factor_of(load1(rAf, row_l + i * 16)) : 1.0f;
+        });
+        static_for<T::FN>([&](auto j) {
+            const int c = col_w + j * 16;
+            if (c < p.N) {
+                const uint32_t bytes = (uint32_t)load4(rBf, c + colq);
+                float fb[4];
+                for (int q = 0; q < 4; ++q) fb[q] = has_f ? factor_of(bytes >> (8 * q)) : 1.0f;
+                static_for<T::FM>([&](auto i) {
+                    f32x4 v = acc[i][j];
+                    for (int q = 0; q < 4; ++q) v[q] = v[q] * (fa[i] * fb[q]);
+                    store8(rO, (uint32_t)(((row_l + i * 16) * p.N + c + colq) * 2),
+                           pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                });
+            }
+        });
+    }
+}
+
+// ======================================================================
+// Skinny (decode) kernel: M <= 16*MT, MT in {1,2}
+// ======================================================================
+template <int MT, int NWK, int U, bool SPLIT>
+__global__ void __launch_bounds__(128 * NWK) gemm_skinny_kernel(const GemmArgs p)
+{
+    static_assert(U % 2 == 0, "batch must cover whole 256-K scale groups");
+    __shared__ f32x4 red[NWK][2][MT][64];
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nf = w & 1, kw = w >> 1;
+    const int n0 = blockIdx.x * 32;
+    const int split = blockIdx.y;
+
+    const int K = p.K, Kp = K >> 1;
+    const int S_total = (K + 127) >> 7;
+    const int s_begin = split * p.sps;
+    const int s_end = min(s_begin + p.sps, S_total);
+    const int n_st = s_end - s_begin;
+    const int CH = (((n_st + NWK - 1) / NWK) + 1) & ~1;
+    const int my_begin = s_begin + kw * CH;
+    const int my_end = min(my_begin + CH, s_end);
+
+    const int nrow = n0 + nf * 16;
+    const bool nvalid = nrow < p.N;
+    const rsrc_t rB = make_rsrc(p.B + (size_t)(nrow >> 4) * K * 8, nvalid ? (uint32_t)(K * 8) : 0u);
+    const rsrc_t rA = make_rsrc(p.A, (uint32_t)(p.M * Kp));
+    const rsrc_t rAs = make_rsrc(p.As, (uint32_t)(32 * p.snp));
+    const rsrc_t rBs = make_rsrc(p.Bs + (size_t)(n0 >> 5) * 32 * p.snp, (uint32_t)(32 * p.snp));
+    const bool hi_lane = lane >= 32;
+    const bool ktail = (K & 127) != 0;
+    const int sshift = 8 * nf;  // B scale byte of this 16-row half
+
+    f32x4 acc[MT];
+    static_for<MT>([&](auto m) { acc[m] = f32x4{0.f, 0.f, 0.f, 0.f}; });
+
+    for (int st = my_begin; st < my_end; st += U) {
+        i32x4 b[U], a[U][MT];
+        int sb[U / 2], sa[U / 2];
+        static_for<U>([&](auto u) {
+            const int s = st + u;
+            const bool ok = s < my_end;
+            const bool zap = (ktail && s == S_total - 1 && hi_lane) || !ok;
+            b[u] = load16(rB, zap ? kOOB : (uint32_t)(s * 1024 + lane * 16));
+            static_for<MT>([&](auto m) {
+                a[u][m] = load16(rA, zap ? kOOB
+                                         : (uint32_t)((16 * m + (lane & 15)) * Kp + s * 64 +
+                                                      (lane >> 4) * 16));
+            });
+        });
+        static_for<U / 2>([&](auto v) {
+            const int g = (st >> 1) + v;
+            const bool ok = st + 2 * v < my_end;
+            sb[v] = load4(rBs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
+            sa[v] = load4(rAs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
+        });
+        static_for<U>([&](auto u) {
+            constexpr int h = u & 1;
+            const int s = st + u;
+            int sbv = sb[u / 2] >> sshift;
+            int sav = sa[u / 2];
+            const bool tail = ktail && s == S_total - 1 && hi_lane;
+            sbv = tail ? 0x7F7F7F7F : sbv;
+            sav = tail ? 0x7F7F7F7F : sav;
+            static_for<MT>([&](auto m) {
+                mfma_fp4<2 * h, m + 2 * h>(acc[m], b[u], a[u][m], sbv, sav);
+            });
+        });
+    }
+
+    mfma_drain();
+    static_for<MT>([&](auto m) { red[kw][nf][m][lane] = acc[m]; });
+    __syncthreads();
+    if (kw != 0 || !nvalid) return;
+
+    const int colq = (lane >> 4) * 4;
+    const int c = nrow + colq;
+    static_for<MT>([&](auto m) {
+        f32x4 v = red[0][nf][m][lane];
+        for (int k = 1; k < NWK; ++k) v += red[k][nf][m][lane];
+        const int row = 16 * m + (lane & 15);
+        if constexpr (SPLIT) {
+            const rsrc_t rW = make_rsrc(p.ws + (size_t)split * p.M * p.N, (uint32_t)(p.M * p.N * 4));
+            store16(rW, (uint32_t)((row * p.N + c) * 4), v);
+        } else {
+            if (p.Af && p.Bf) {
+                const rsrc_t rAf = make_rsrc(p.Af, (uint32_t)p.M);
+                const rsrc_t rBf = make_rsrc(p.Bf, (uint32_t)p.N);
+                const float fa = factor_of(load1(rAf, row));
+                const uint32_t bytes = (uint32_t)load4(rBf, c);
+                for (int q = 0; q < 4; ++q) v[q] = v[q] * (fa * factor_of(bytes >> (8 * q)));
+            }
+            const rsrc_t rO = make_rsrc(p.out, (uint32_t)(p.M * p.N * 2));
+            store8(rO, (uint32_t)((row * p.N + c) * 2), pack_bf16x2(v[0], v[1]),
+                   pack_bf16x2(v[2], v[3]));
+        }
+    });
+}
+
+// ======================================================================
+// Split-K reduction: out[m][n..n+3] = epilogue(sum_s ws[s][m][n..n+3])
+// ======================================================================
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs p)
+{
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int nq = p.N >> 2;
+    if (q >= (int64_t)p.M * nq) return;
+    const int m = (int)(q / nq);
+    const int c = (int)(q - (int64_t)m * nq) * 4;
+    const size_t plane = (size_t)p.M * p.N;
+    const f32x4* src = reinterpret_cast<const f32x4*>(p.ws + (size_t)m * p.N + c);
+    f32x4 v = src[0];
+    for (int s = 1; s < p.splits; ++s) v += *reinterpret_cast<const f32x4*>(p.ws + s * plane + (size_t)m * p.N + c);
+    if (p.Af && p.Bf) {
+        const float fa = factor_of(p.Af[m]);
+        const uint32_t bytes = *reinterpret_cast<const uint32_t*>(p.Bf + c);
+        for (int k = 0; k < 4; ++k) v[k] = v[k] * (fa * factor_of(bytes >> (8 * k)));
+    }
+    uint32_t* o = reinterpret_cast<uint32_t*>(p.out + (size_t)m * p.N + c);
+    o[0] = pack_bf16x2(v[0], v[1]);
+    o[1] = pack_bf16x2(v[2], v[3]);
+}
+
+// ======================================================================
+// Host side: configurations, plans, launch
+// ======================================================================
+namespace {
+
+int fail(int code, const std::string& msg)
+{
+    set_last_error(msg.c_str());
+    return code;
+}
+
+enum Family { kTiled = 0, kSkinny = 1 };
+
+struct Config {
+    const char* name;
+    Family family;
+    int bm, bn;        // tiled: workgroup tile; skinny: rows covered (16*MT) x 32
+    int threads;
+    int wgs_per_cu;    // resident workgroups per CU (LDS / register bound)
+    float eff;         // relative per-CU throughput of the tile (cost model)
+    // launch(args, grid, ktail, split, stream)
+    hipError_t (*launch)(const GemmArgs&, dim3, bool, bool, hipStream_t);
+};
+
+template <class T>
+hipError_t launch_tiled(const GemmArgs& a, dim3 grid, bool ktail, bool split, hipStream_t s)
+{
+    if (ktail) {
+        if (split) hipLaunchKernelGGL((gemm_tiled_kernel<T, true, true>), grid, dim3(T::NT), 0, s, a);
+        else hipLaunchKernelGGL((gemm_tiled_kernel<T, true, false>), grid, dim3(T::NT), 0, s, a);
+    } else {
+        if (split) hipLaunchKernelGGL((gemm_tiled_kernel<T, false, true>), grid, dim3(T::NT), 0, s, a);
+        else hipLaunchKernelGGL((gemm_tiled_kernel<T, false, false>), grid, dim3(T::NT), 0, s, a);
+    }
+    return hipGetLastError();
+}
+
+template <int MT, int NWK, int U>
+hipError_t launch_skinny(const GemmArgs& a, dim3 grid, bool, bool split, hipStream_t s)
+{
+    if (split) hipLaunchKernelGGL((gemm_skinny_kernel<MT, NWK, U, true>), grid, dim3(128 * NWK), 0, s, a);
+    else hipLaunchKernelGGL((gemm_skinny_kernel<MT, NWK, U, false>), grid, dim3(128 * NWK), 0, s, a);
+    return hipGetLastError();
+}
+
+using T256x256 = TileShape<256, 256, 2, 2>;
+using T256x128 = TileShape<256, 128, 2, 2>;
+using T128x256 = TileShape<128, 256, 2, 2>;
+using T128x128 = TileShape<128, 128, 2, 2>;
+using T64x256 = TileShape<64, 256, 1, 4>;
+using T64x128 = TileShape<64, 128, 1, 2>;
+using T64x64 = TileShape<64, 64, 1, 1>;
+
+const Config kConfigs[] = {
+    {"tiled_256x256_w2x2", kTiled, 256, 256, 256, 1, 1.00f, launch_tiled<T256x256>},
+    {"tiled_256x128_w2x2", kTiled, 256, 128, 256, 1, 0.85f, launch_tiled<T256x128>},
+    {"tiled_128x256_w2x2", kTiled, 128, 256, 256, 1, 0.85f, launch_tiled<T128x256>},
+    {"tiled_128x128_w2x2", kTiled, 128, 128, 256, 2, 0.70f, launch_tiled<T128x128>},
+    {"tiled_64x256_w1x4", kTiled, 64, 256, 256, 2, 0.65f, launch_tiled<T64x256>},
+    {"tiled_64x128_w1x2", kTiled, 64, 128, 128, 3, 0.50f, launch_tiled<T64x128>},
+    {"tiled_64x64_w1x1", kTiled, 64, 64, 64, 4, 0.35f, launch_tiled<T64x64>},
+    {"skinny_m16_k8", kSkinny, 16, 32, 1024, 1, 1.0f, launch_skinny<1, 8, 8>},
+    {"skinny_m32_k8", kSkinny, 32, 32, 1024, 1, 1.0f, launch_skinny<2, 8, 8>},
+    {"skinny_m16_k4", kSkinny, 16, 32, 512, 2, 1.0f, launch_skinny<1, 4, 8>},
+    {"skinny_m32_k4", kSkinny, 32, 32, 512, 2, 1.0f, launch_skinny<2, 4, 8>},
+};
+constexpr int kNumConfigs = (int)(sizeof(kConfigs) / sizeof(kConfigs[0]));
+constexpr int kNumCUs = 256;
+
+struct Plan {
+    int config;
+    int splits;
+    int sps;
+    dim3 grid;
+    size_t ws_bytes;
+};
+
+int stages_of(int K) { return (K + 127) / 128; }
+
+// Split count -> stages per split (even) and the realised split count.
+void split_stages(int K, int want, int* sps, int* splits)
+{
+    const int S = stages_of(K);
+    int per = (S + want - 1) / want;
+    per = (per + 1) & ~1;
+    if (per < 2) per = 2;
+    *sps = per;
+    *splits = (S + per - 1) / per;
+}
+
+bool make_plan(int config, int want_splits, int M, int N, int K, Plan* out)
+{
+    if (config < 0 || config >= kNumConfigs) return false;
+    const Config& c = kConfigs[config];
+    Plan pl{};
+    pl.config = config;
+    if (c.family == kSkinny) {
+        if (M > c.bm) return false;
+        const int wgs = (N + 31) / 32;
+        int want = want_splits;
+        if (want <= 0) {
+            // aim for ~8 resident waves per CU of 16-row B streams
+            const int waves = wgs * (c.threads / 64);
+            want = std::max(1, (kNumCUs * 8) / std::max(1, waves));
+            want = std::min(want, std::max(1, stages_of(K) / (2 * (c.threads / 128))));
+        }
+        split_stages(K, want, &pl.sps, &pl.splits);
+        pl.grid = dim3(wgs, pl.splits, 1);
+    } else {
+        const int tm = (M + c.bm - 1) / c.bm, tn = (N + c.bn - 1) / c.bn;
+        int want = want_splits;
+        if (want <= 0) {
+            const int slots = kNumCUs * c.wgs_per_cu;
+            want = 1;
+            // split K while the grid fills less than half the resident slots
+            while (tm * tn * want * 2 <= slots && stages_of(K) / (want * 2) >= 4) want *= 2;
+        }
+        split_stages(K, want, &pl.sps, &pl.splits);
+        pl.grid = dim3(tm * tn * pl.splits, 1, 1);
+    }
+    pl.ws_bytes = pl.splits > 1 ? (size_t)pl.splits * M * N * 4 : 0;
+    *out = pl;
+    return true;
+}
+
+// Cost model: estimated time in ns.  Per-CU dense fp4 MFMA rate is
+// 4 SIMD x 4096 flop/clk x 2.4 GHz = 39322 flop/ns; a tile's efficiency
+// `eff` scales it.  Workgroups sharing a CU split its rate.  Split-K adds
+// the partial round trip at ~5 TB/s plus one extra dependent launch.
+constexpr double kCuFlopPerNs = 39322.0;
+constexpr double kHbmBytesPerNs = 6000.0;
+constexpr double kExtraLaunchNs = 2500.0;
+
+double plan_cost(const Plan& pl, int M, int N, int K)
+{
+    const Config& c = kConfigs[pl.config];
+    const double wgs = (double)pl.grid.x * pl.grid.y;
+    const double split_ns =
+        pl.splits > 1 ? (double)pl.ws_bytes * 2.0 / 5000.0 + kExtraLaunchNs : 0.0;
+    const double hbm_ns =
+        ((double)M * K / 2 + (double)N * K / 2 + (double)(M + N) * K / 32 + 2.0 * M * N) /
+        kHbmBytesPerNs;
+    if (c.family == kSkinny) {
+        // bandwidth-bound: needs ~8 waves streaming B per CU to saturate HBM
+        const double waves = wgs * (c.threads / 64);
+        const double occ = std::min(1.0, waves / (kNumCUs * 8.0));
+        return hbm_ns / std::max(occ, 0.02) + split_ns;
+    }
+    const double slots = (double)kNumCUs * c.wgs_per_cu;
+    const double rounds = std::ceil(wgs / slots);
+    const double ksplit = pl.sps * 128.0;
+    const double per_wg_ns = 2.0 * c.bm * c.bn * ksplit * c.wgs_per_cu / (kCuFlopPerNs * c.eff);
+    return std::max(rounds * per_wg_ns, hbm_ns) + split_ns;
+}
+
+bool choose_plan(int M, int N, int K, size_t ws_avail, Plan* best)
+{
+    bool have = false;
+    double best_cost = 0;
+    for (int i = 0; i < kNumConfigs; ++i) {
+        Plan pl;
+        if (!make_plan(i, 0, M, N, K, &pl)) continue;
+        if (pl.ws_bytes > ws_avail || pl.ws_bytes >= (1ull << 31)) {
+            if (!make_plan(i, 1, M, N, K, &pl)) continue;
+        }
+        const double cst = plan_cost(pl, M, N, K);
+        if (!have || cst < best_cost) {
+            *best = pl;
+            best_cost = cst;
+            have = true;
+        }
+    }
+    return have;
+}
+
+int validate(const uint8_t* A, const uint8_t* B, const uint8_t* As, const uint8_t* Bs,
+             const uint8_t* Af, const uint8_t* Bf, void* out, int M, int N, int K, int Mpad,
+             int snp)
+{
+    if (!A || !B || !As || !Bs || !out) return fail(MBS_ERR_ARGUMENT, "null operand pointer");
+    if ((Af == nullptr) != (Bf == nullptr))
+        return fail(MBS_ERR_ARGUMENT, "AFactor and BFactor must be given together");
+    if (M < 1 || N < 16 || K < 64)
+        return fail(MBS_ERR_ARGUMENT, "need M >= 1, N >= 16, K >= 64; got M=" + std::to_string(M) +
+                                          " N=" + std::to_string(N) + " K=" + std::to_string(K));
+    if (N % 16) return fail(MBS_ERR_ARGUMENT, "N must be a multiple of 16, got " + std::to_string(N));
+    if (K % 64)
+        return fail(MBS_ERR_ARGUMENT, "K must be a multiple of 64 (16x16 B preshuffle), got " +
+                                          std::to_string(K));
+    if (Mpad != (M + 31) / 32 * 32)
+        return fail(MBS_ERR_ARGUMENT, "Mpad must be round_up(M, 32)");
+    if (snp != ((K + 31) / 32 + 7) / 8 * 8)
+        return fail(MBS_ERR_ARGUMENT, "scaleN_pad must be round_up(ceil(K/32), 8)");
+    if ((int64_t)256 * (K / 2) >= (1ll << 31) || (int64_t)256 * N * 4 >= (1ll << 31) ||
+        (int64_t)M * (K / 2) >= (1ll << 31) || (int64_t)M * N * 4 >= (1ll << 31))
+        return fail(MBS_ERR_ARGUMENT, "problem too large for 32-bit buffer offsets");
+    return MBS_OK;
+}
+
+int run_plan(const Plan& pl, const uint8_t* A, const uint8_t* B, const uint8_t* As,
+             const uint8_t* Bs, const uint8_t* Af, const uint8_t* Bf, void* out, int M, int N,
+             int K, int snp, void* ws, size_t ws_bytes, void* stream)
+{
+    const Config& c = kConfigs[pl.config];
+    if (pl.ws_bytes > ws_bytes || (pl.ws_bytes && !ws))
+        return fail(MBS_ERR_WORKSPACE, "workspace too small: need " + std::to_string(pl.ws_bytes) +
+                                           " bytes");
+    GemmArgs a{};
+    a.A = A; a.B = B; a.As = As; a.Bs = Bs; a.Af = Af; a.Bf = Bf;
+    a.out = static_cast<uint16_t*>(out);
+    a.ws = static_cast<float*>(ws);
+    a.M = M; a.N = N; a.K = K; a.snp = snp;
+    a.tiles_m = (M + c.bm - 1) / c.bm;
+    a.tiles_n = (N + c.bn - 1) / c.bn;
+    a.splits = pl.splits;
+    a.sps = pl.sps;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    (void)hipGetLastError();  // do not report a stale error as ours
+    hipError_t e = c.launch(a, pl.grid, (K % 128) != 0, pl.splits > 1, s);
+    if (e != hipSuccess) return fail(MBS_ERR_LAUNCH, std::string("launch failed: ") + hipGetErrorString(e));
+    if (pl.splits > 1) {
+        const int64_t quads = (int64_t)M * (N / 4);
+        dim3 g((unsigned)((quads + 255) / 256));
+        hipLaunchKernelGGL(splitk_reduce_kernel, g, dim3(256), 0, s, a);
+        e = hipGetLastError();
+        if (e != hipSuccess)
+            return fail(MBS_ERR_LAUNCH, std::string("reduce launch failed: ") + hipGetErrorString(e));
+    }
+    return MBS_OK;
+}
+
+}  // namespace
+}  // namespace mbs
+
+using namespace mbs;
+
+extern "C" {
+
+const char* mbs_status_string(int status)
+{
+    switch (status) {
+    case MBS_OK: return "ok";
+    case MBS_ERR_ARGUMENT: return "invalid argument";
+    case MBS_ERR_WORKSPACE: return "workspace too small";
+    case MBS_ERR_LAUNCH: return "kernel launch failed";
+    case MBS_ERR_CONFIG: return "invalid kernel configuration";
+    default: return "unknown status";
+    }
+}
+
+const char* mbs_last_error(void) { return g_last_error.c_str(); }
+
+size_t mbs_gemm_a4w4_workspace_bytes(int M, int N, int K)
+{
+    if (M < 1 || N < 16 || K < 64 || N % 16 || K % 64) return 0;
+    Plan pl;
+    if (!choose_plan(M, N, K, (size_t)1 << 31, &pl)) return 0;
+    return pl.ws_bytes;
+}
+
+int mbs_gemm_a4w4_launch(const uint8_t* A, const uint8_t* B, const uint8_t* AScale,
+                         const uint8_t* BScale, const uint8_t* AFactor, const uint8_t* BFactor,
+                         void* out, int M, int N, int K, int Mpad, int scaleN_pad,
+                         void* workspace, size_t workspace_bytes, void* stream)
+{
+    set_last_error("");
+    int st = validate(A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, Mpad, scaleN_pad);
+    if (st != MBS_OK) return st;
+    Plan pl;
+    if (!choose_plan(M, N, K, workspace ? workspace_bytes : 0, &pl))
+        return fail(MBS_ERR_CONFIG, "no kernel configuration fits this problem");
+    return run_plan(pl, A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, scaleN_pad,
+                    workspace, workspace_bytes, stream);
+}
+
+int mbs_gemm_a4w4_num_configs(void) { return kNumConfigs; }
+
+const char* mbs_gemm_a4w4_config_name(int config)
+{
+    return (config >= 0 && config < kNumConfigs) ? kConfigs[config].name : "";
+}
+
+int mbs_gemm_a4w4_plan_name(int M, int N, int K, char* buf, size_t buf_len)
+{
+    Plan pl;
+    if (M < 1 || N < 16 || K < 64 || N % 16 || K % 64 || !choose_plan(M, N, K, (size_t)1 << 31, &pl))
+        return MBS_ERR_ARGUMENT;
+    if (buf && buf_len)
+        snprintf(buf, buf_len, "%s splits=%d grid=%ux%u ws=%zu", kConfigs[pl.config].name,
+                 pl.splits, pl.grid.x, pl.grid.y, pl.ws_bytes);
+    return MBS_OK;
+}
+
+size_t mbs_gemm_a4w4_config_workspace_bytes(int config, int splits, int M, int N, int K)
+{
+    Plan pl;
+    if (!make_plan(config, splits, M, N, K, &pl)) return 0;
+    return pl.ws_bytes;
+}
+
+int mbs_gemm_a4w4_launch_config(int config, int splits, const uint8_t* A, const uint8_t* B,
+                                const uint8_t* AScale, const uint8_t* BScale,
+                                const uint8_t* AFactor, const uint8_t* BFactor, void* out, int M,
+                                int N, int K, int Mpad, int scaleN_pad, void* workspace,
+                                size_t workspace_bytes, void* stream)
+{
+    set_last_error("");
+    int st = validate(A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, Mpad, scaleN_pad);
+    if (st != MBS_OK) return st;
+    Plan pl;
+    if (!make_plan(config, splits, M, N, K, &pl))
+        return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) + " cannot run M=" +
+                                        std::to_string(M));
+    return run_plan(pl, A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, scaleN_pad,
+                    workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"

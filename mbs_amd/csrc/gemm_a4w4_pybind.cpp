@@ -1,0 +1,254 @@
+// Torch-facing module `mbs_gemm_a4w4`: the drop-in for the reference's
+// pybind entry (interface/gemm_a4w4_pybind.cpp:19-74 of the reference).
+//
+// gemm_a4w4(A, B, A_scale, B_scale, A_factor=None, B_factor=None) validates
+// the operands, allocates the [Mpad, N] bf16 output (and any split-K
+// workspace) through torch's caching allocator, and launches on the current
+// HIP stream through the C ABI of libmbs_gemm_kernel.so.  It returns the
+// [M, N] view of the padded output, as the reference does.  The factors are
+// optional here (the reference requires them, which makes its own
+// bench_one.py 4-argument call fail); omitting them means "no scaling".
+//
+// The format helpers (quantize, preshuffle, dequantize) are exported too, so
+// a caller needs nothing beyond this module to prepare operands.
+#include <torch/extension.h>
+
+#include <c10/hip/HIPGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <string>
+
+#include "mbs_gemm_a4w4.h"
+
+namespace {
+
+void* current_stream(const at::Tensor& t)
+{
+    return reinterpret_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+void check_status(int st, const char* what)
+{
+    TORCH_CHECK(st == MBS_OK, what, ": ", mbs_status_string(st), " (", mbs_last_error(), ")");
+}
+
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+int64_t scale_pad(int64_t K) { return round_up((K + 31) / 32, 8); }
+
+at::Tensor as_bytes(const at::Tensor& t) { return t.view(at::kByte).contiguous(); }
+
+struct Operands {
+    at::Tensor A, B, As, Bs, Af, Bf;
+    int M = 0, N = 0, K = 0, Mpad = 0, snp = 0;
+    bool factors = false;
+};
+
+Operands prepare(const at::Tensor& A, const at::Tensor& B, const at::Tensor& A_scale,
+                 const at::Tensor& B_scale, const c10::optional<at::Tensor>& A_factor,
+                 const c10::optional<at::Tensor>& B_factor)
+{
+    TORCH_CHECK(A.is_cuda() && B.is_cuda(), "gemm_a4w4: A, B must be on device");
+    TORCH_CHECK(A.dim() == 2 && B.dim() == 2, "gemm_a4w4: A, B must be 2D");
+    TORCH_CHECK(A_scale.is_cuda() && B_scale.is_cuda(), "gemm_a4w4: scales must be on device");
+    TORCH_CHECK(A.element_size() == 1 && B.element_size() == 1 && A_scale.element_size() == 1 &&
+                    B_scale.element_size() == 1,
+                "gemm_a4w4: A, B and the scales must have a 1-byte dtype");
+    const auto dev = A.device();
+    TORCH_CHECK(B.device() == dev && A_scale.device() == dev && B_scale.device() == dev,
+                "gemm_a4w4: all operands must be on the same device");
+    Operands o;
+    o.A = as_bytes(A);
+    o.B = as_bytes(B);
+    o.As = as_bytes(A_scale);
+    o.Bs = as_bytes(B_scale);
+    o.M = (int)o.A.size(0);
+    const int64_t Kp = o.A.size(1);
+    o.K = (int)(Kp * 2);
+    o.N = (int)o.B.size(0);
+    TORCH_CHECK(o.B.size(1) == Kp, "gemm_a4w4: A, B must share K/2, got ", o.A.size(1), " vs ",
+                o.B.size(1));
+    TORCH_CHECK(o.M >= 1, "gemm_a4w4: M must be >= 1");
+    TORCH_CHECK(o.K % 32 == 0, "gemm_a4w4: K must be a multiple of 32, got ", o.K);
+    TORCH_CHECK(o.K % 64 == 0, "gemm_a4w4: K must be a multiple of 64 (the (16,16) B preshuffle "
+                "groups 32 bytes of K), got ", o.K);
+    TORCH_CHECK(o.N % 16 == 0, "gemm_a4w4: N must be a multiple of 16, got ", o.N);
+    o.Mpad = (int)round_up(o.M, 32);
+    o.snp = (int)scale_pad(o.K);
+    TORCH_CHECK(o.As.numel() >= (int64_t)o.Mpad * o.snp, "gemm_a4w4: A_scale must hold at least ",
+                (int64_t)o.Mpad * o.snp, " bytes (round_up(M,32) * scaleN_pad), got ",
+                o.As.numel());
+    TORCH_CHECK(o.Bs.numel() >= round_up(o.N, 32) * o.snp, "gemm_a4w4: B_scale must hold at least ",
+                round_up(o.N, 32) * o.snp, " bytes (round_up(N,32) * scaleN_pad), got ",
+                o.Bs.numel());
+    const bool has_a = A_factor.has_value() && A_factor->defined();
+    const bool has_b = B_factor.has_value() && B_factor->defined();
+    TORCH_CHECK(has_a == has_b, "gemm_a4w4: A_factor and B_factor must be given together");
+    o.factors = has_a;
+    if (o.factors) {
+        o.Af = as_bytes(*A_factor);
+        o.Bf = as_bytes(*B_factor);
+        TORCH_CHECK(o.Af.is_cuda() && o.Af.numel() == o.M, "gemm_a4w4: A_factor must hold M = ",
+                    o.M, " bytes on device, got ", o.Af.numel());
+        TORCH_CHECK(o.Bf.is_cuda() && o.Bf.numel() == o.N, "gemm_a4w4: B_factor must hold N = ",
+                    o.N, " bytes on device, got ", o.Bf.numel());
+        TORCH_CHECK(o.Af.device() == dev && o.Bf.device() == dev,
+                    "gemm_a4w4: factors must be on the operands' device");
+    }
+    return o;
+}
+
+at::Tensor run(const Operands& o, int config, int splits)
+{
+    c10::hip::HIPGuard guard(o.A.device());
+    auto out = torch::empty({o.Mpad, o.N},
+                            torch::TensorOptions().dtype(torch::kBFloat16).device(o.A.device()));
+    const size_t ws = config < 0 ? mbs_gemm_a4w4_workspace_bytes(o.M, o.N, o.K)
+                                 : mbs_gemm_a4w4_config_workspace_bytes(config, splits, o.M, o.N, o.K);
+    at::Tensor wst;
+    if (ws) wst = torch::empty({(int64_t)ws}, torch::TensorOptions().dtype(torch::kByte).device(o.A.device()));
+    const uint8_t* af = o.factors ? o.Af.data_ptr<uint8_t>() : nullptr;
+    const uint8_t* bf = o.factors ? o.Bf.data_ptr<uint8_t>() : nullptr;
+    void* s = current_stream(o.A);
+    int st;
+    if (config < 0)
+        st = mbs_gemm_a4w4_launch(o.A.data_ptr<uint8_t>(), o.B.data_ptr<uint8_t>(),
+                                  o.As.data_ptr<uint8_t>(), o.Bs.data_ptr<uint8_t>(), af, bf,
+                                  out.data_ptr(), o.M, o.N, o.K, o.Mpad, o.snp,
+                                  ws ? wst.data_ptr() : nullptr, ws, s);
+    else
+        st = mbs_gemm_a4w4_launch_config(config, splits, o.A.data_ptr<uint8_t>(),
+                                         o.B.data_ptr<uint8_t>(), o.As.data_ptr<uint8_t>(),
+                                         o.Bs.data_ptr<uint8_t>(), af, bf, out.data_ptr(), o.M,
+                                         o.N, o.K, o.Mpad, o.snp, ws ? wst.data_ptr() : nullptr,
+                                         ws, s);
+    check_status(st, "gemm_a4w4");
+    return out.narrow(0, 0, o.M);
+}
+
+}  // namespace
+
+// The reference's operator (interface/gemm_a4w4_pybind.cpp:19-64).
+at::Tensor gemm_a4w4(at::Tensor A, at::Tensor B, at::Tensor A_scale, at::Tensor B_scale,
+                     c10::optional<at::Tensor> A_factor, c10::optional<at::Tensor> B_factor)
+{
+    return run(prepare(A, B, A_scale, B_scale, A_factor, B_factor), -1, 0);
+}
+
+// Same operator with a forced kernel configuration (tests, tuning).
+at::Tensor gemm_a4w4_config(int64_t config, int64_t splits, at::Tensor A, at::Tensor B,
+                            at::Tensor A_scale, at::Tensor B_scale,
+                            c10::optional<at::Tensor> A_factor,
+                            c10::optional<at::Tensor> B_factor)
+{
+    TORCH_CHECK(config >= 0 && config < mbs_gemm_a4w4_num_configs(), "gemm_a4w4_config: config ",
+                config, " out of range [0, ", mbs_gemm_a4w4_num_configs(), ")");
+    return run(prepare(A, B, A_scale, B_scale, A_factor, B_factor), (int)config, (int)splits);
+}
+
+// bf16 [R, K] -> (packed u8 [R, K/2], scales).  shuffle=True returns the
+// shuffled scale buffer viewed as [round_up(R,32), scaleN_pad]; False returns
+// plain [R, K/32] scales (the two quantizer modes of test_gemm_a4w4.py:137-140).
+std::tuple<at::Tensor, at::Tensor> quantize_mxfp4(at::Tensor x, bool shuffle, int64_t pad_byte)
+{
+    TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.scalar_type() == at::kBFloat16,
+                "quantize_mxfp4: x must be a 2D bf16 device tensor");
+    auto xc = x.contiguous();
+    const int64_t R = xc.size(0), K = xc.size(1);
+    TORCH_CHECK(K % 32 == 0, "quantize_mxfp4: K must be a multiple of 32");
+    c10::hip::HIPGuard guard(x.device());
+    auto opts = torch::TensorOptions().dtype(torch::kByte).device(x.device());
+    auto packed = torch::empty({R, K / 2}, opts);
+    at::Tensor scales = shuffle ? torch::empty({round_up(R, 32), scale_pad(K)}, opts)
+                                : torch::empty({R, K / 32}, opts);
+    check_status(mbs_quantize_mxfp4_bf16(xc.data_ptr(), (int)R, (int)K, packed.data_ptr<uint8_t>(),
+                                         shuffle ? scales.data_ptr<uint8_t>() : nullptr,
+                                         shuffle ? nullptr : scales.data_ptr<uint8_t>(),
+                                         (int)pad_byte, current_stream(x)),
+                 "quantize_mxfp4");
+    return {packed, scales};
+}
+
+// Plain packed weights [N, K/2] -> (16,16)-preshuffled copy (shuffle_weight).
+at::Tensor shuffle_weight(at::Tensor w)
+{
+    TORCH_CHECK(w.is_cuda() && w.dim() == 2 && w.element_size() == 1,
+                "shuffle_weight: w must be a 2D 1-byte device tensor");
+    auto wu = as_bytes(w);
+    c10::hip::HIPGuard guard(w.device());
+    auto out = torch::empty_like(wu);
+    check_status(mbs_shuffle_b(wu.data_ptr<uint8_t>(), out.data_ptr<uint8_t>(), (int)wu.size(0),
+                               (int)(wu.size(1) * 2), current_stream(w)),
+                 "shuffle_weight");
+    return out;
+}
+
+// Plain E8M0 [R, K/32] -> shuffled [round_up(R,32), scaleN_pad].
+at::Tensor shuffle_scales(at::Tensor s, int64_t pad_byte)
+{
+    TORCH_CHECK(s.is_cuda() && s.dim() == 2 && s.element_size() == 1,
+                "shuffle_scales: s must be a 2D 1-byte device tensor");
+    auto su = as_bytes(s);
+    const int64_t R = su.size(0), K = su.size(1) * 32;
+    c10::hip::HIPGuard guard(s.device());
+    auto out = torch::empty({round_up(R, 32), scale_pad(K)},
+                            torch::TensorOptions().dtype(torch::kByte).device(s.device()));
+    check_status(mbs_shuffle_scales(su.data_ptr<uint8_t>(), out.data_ptr<uint8_t>(), (int)R, (int)K,
+                                    (int)pad_byte, current_stream(s)),
+                 "shuffle_scales");
+    return out;
+}
+
+// Packed operand + shuffled scales -> fp32 [R, K] (mxfp4_to_f32 * e8m0_to_f32).
+at::Tensor dequant_mxfp4(at::Tensor packed, at::Tensor scale_shuffled, bool b_preshuffled)
+{
+    TORCH_CHECK(packed.is_cuda() && packed.dim() == 2 && packed.element_size() == 1,
+                "dequant_mxfp4: packed must be a 2D 1-byte device tensor");
+    TORCH_CHECK(scale_shuffled.is_cuda() && scale_shuffled.element_size() == 1,
+                "dequant_mxfp4: scales must be a 1-byte device tensor");
+    auto pu = as_bytes(packed);
+    auto su = as_bytes(scale_shuffled);
+    const int64_t R = pu.size(0), K = pu.size(1) * 2;
+    TORCH_CHECK(su.numel() >= round_up(R, 32) * scale_pad(K), "dequant_mxfp4: scale buffer too small");
+    c10::hip::HIPGuard guard(packed.device());
+    auto out = torch::empty({R, K}, torch::TensorOptions().dtype(torch::kFloat32).device(packed.device()));
+    check_status(mbs_dequant_mxfp4(pu.data_ptr<uint8_t>(), su.data_ptr<uint8_t>(),
+                                   out.data_ptr<float>(), (int)R, (int)K, b_preshuffled ? 1 : 0,
+                                   current_stream(packed)),
+                 "dequant_mxfp4");
+    return out;
+}
+
+std::string plan_name(int64_t M, int64_t N, int64_t K)
+{
+    char buf[256];
+    check_status(mbs_gemm_a4w4_plan_name((int)M, (int)N, (int)K, buf, sizeof(buf)), "plan_name");
+    return buf;
+}
+
+PYBIND11_MODULE(mbs_gemm_a4w4, m)
+{
+    m.doc() = "MI355X (gfx950) MXFP4 A4W4 GEMM";
+    m.def("gemm_a4w4", &gemm_a4w4,
+          "MXFP4 A4W4 GEMM: out[M,N] = dequant(A) @ dequant(B)^T [* f(A_factor) * f(B_factor)^T]",
+          pybind11::arg("A"), pybind11::arg("B"), pybind11::arg("A_scale"),
+          pybind11::arg("B_scale"), pybind11::arg("A_factor") = pybind11::none(),
+          pybind11::arg("B_factor") = pybind11::none());
+    m.def("gemm_a4w4_config", &gemm_a4w4_config, "gemm_a4w4 with a forced kernel configuration",
+          pybind11::arg("config"), pybind11::arg("splits"), pybind11::arg("A"), pybind11::arg("B"),
+          pybind11::arg("A_scale"), pybind11::arg("B_scale"),
+          pybind11::arg("A_factor") = pybind11::none(), pybind11::arg("B_factor") = pybind11::none());
+    m.def("quantize_mxfp4", &quantize_mxfp4, "bf16 -> (packed e2m1, E8M0 scales)",
+          pybind11::arg("x"), pybind11::arg("shuffle") = true, pybind11::arg("pad_byte") = 127);
+    m.def("shuffle_weight", &shuffle_weight, "(16,16) preshuffle of packed weights",
+          pybind11::arg("w"));
+    m.def("shuffle_scales", &shuffle_scales, "plain -> shuffled E8M0 scales", pybind11::arg("s"),
+          pybind11::arg("pad_byte") = 127);
+    m.def("dequant_mxfp4", &dequant_mxfp4, "packed + shuffled scales -> fp32",
+          pybind11::arg("packed"), pybind11::arg("scale"), pybind11::arg("b_preshuffled") = false);
+    m.def("plan_name", &plan_name, "kernel plan the heuristic picks for (M, N, K)");
+    m.def("num_configs", []() { return mbs_gemm_a4w4_num_configs(); });
+    m.def("config_name", [](int64_t c) { return std::string(mbs_gemm_a4w4_config_name((int)c)); });
+    m.def("workspace_bytes", [](int64_t M, int64_t N, int64_t K) {
+        return (int64_t)mbs_gemm_a4w4_workspace_bytes((int)M, (int)N, (int)K);
+    });
+}

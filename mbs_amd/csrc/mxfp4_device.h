@@ -1,0 +1,180 @@
+// Device helpers shared by the gfx950 MXFP4 kernels: vector types, buffer
+// resources, LDS DMA, the block-scaled fp4 MFMA, waits and barriers, the MBS
+// factor table and bf16 packing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <utility>
+
+namespace mbs {
+
+// Records the text mbs_last_error() returns (thread-local, host side).
+void set_last_error(const char* msg);
+
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+#define MBS_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// Offset that is out of range for every buffer resource built here
+// (num_records is always < 2^31): a load through it returns 0, a store is
+// dropped.
+constexpr uint32_t kOOB = 0x80000000u;
+
+// ------------------------------------------------------- compile-time loops
+template <int... Is, class F>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, Is...>, F&& f)
+{
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f)
+{
+    static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
+
+// ------------------------------------------------------- buffer resources
+// Raw (stride 0) buffer over `bytes` bytes from `base`.  Word 3 = 0x00020000
+// is the gfx9 raw-buffer format (32-bit data format, no swizzle); accesses at
+// offsets >= bytes read as 0 / are discarded.
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+// 16-byte global->LDS DMA: lane i's 16 bytes at `voffset` land at
+// lds + 16*i (M0 = lds).  soffset is kept 0 so the range check sees the whole
+// offset.
+__device__ __forceinline__ void dma16(rsrc_t r, void* lds, uint32_t voffset)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, MBS_LDS_PTR(lds), 16, voffset, 0, 0, 0);
+}
+// 4-byte global->LDS DMA: lane i's dword lands at lds + 4*i.
+__device__ __forceinline__ void dma4(rsrc_t r, void* lds, uint32_t voffset)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, MBS_LDS_PTR(lds), 4, voffset, 0, 0, 0);
+}
+
+__device__ __forceinline__ i32x4 load16(rsrc_t r, uint32_t voffset)
+{
+    return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 0));
+}
+__device__ __forceinline__ int load4(rsrc_t r, uint32_t voffset)
+{
+    return (int)__builtin_amdgcn_raw_buffer_load_b32(r, voffset, 0, 0);
+}
+__device__ __forceinline__ uint32_t load1(rsrc_t r, uint32_t voffset)
+{
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, voffset, 0, 0);
+}
+__device__ __forceinline__ void store8(rsrc_t r, uint32_t voffset, uint32_t lo, uint32_t hi)
+{
+    i32x2 v = {(int)lo, (int)hi};
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned, v), r, voffset, 0, 0);
+}
+__device__ __forceinline__ void store16(rsrc_t r, uint32_t voffset, f32x4 v)
+{
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v), r, voffset, 0, 0);
+}
+__device__ __forceinline__ f32x4 loadf4(rsrc_t r, uint32_t voffset)
+{
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 0));
+}
+
+// ---------------------------------------------------------- waits/barrier
+// s_waitcnt vmcnt(n), leaving expcnt/lgkmcnt unconstrained (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkmcnt0()
+{
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (3 << 14));
+}
+
+// Workgroup barrier with no implied memory fence (the fence of
+// __syncthreads would force vmcnt(0) and drain the LDS DMA prefetch).  The
+// "memory" clobber keeps the compiler from moving LDS accesses across it;
+// callers wait on their own DMA (wait_vmcnt) before arriving.
+__device__ __forceinline__ void barrier()
+{
+    asm volatile("s_barrier" ::: "memory");
+}
+
+// -------------------------------------------------------------- fp4 MFMA
+// acc(16x16, fp32) += A(16x128 e2m1) * B(128x16 e2m1), block-scaled, with
+// v_mfma_scale_f32_16x16x128_f8f6f4 (cbsz = blgp = 4: both operands fp4).
+// Operand layout (both operands): lane L holds row/col (L % 16) and the
+// 32-element K-block (L / 16) as 16 bytes (32 nibbles, low nibble first).
+// Scale: lane L's E8M0 byte for that same (row, K-block); OPA/OPB (0..3) pick
+// the byte of the 32-bit scale register (op_sel bit 0 / op_sel_hi bit 1).
+// Output: acc[t] on lane L is D[(L / 16) * 4 + t][L % 16].
+//
+// Written as inline asm with the accumulator tied to an AGPR ("+a") so every
+// MFMA accumulates in place: with the builtin the register allocator renames
+// accumulators across the unrolled K loop and emits a v_accvgpr copy per MFMA.
+// Because the compiler's hazard recognizer cannot see into the asm, each MFMA
+// starts with s_nop 1: the two wait states gfx9 needs between a VALU write of
+// a VGPR and an MFMA reading it.  (Loads need none: their results are waited
+// for with s_waitcnt.)  Reading the accumulators after the last MFMA needs the
+// wait of mfma_drain().
+template <int OPA, int OPB>
+__device__ __forceinline__ void mfma_fp4(f32x4& acc, i32x4 a, i32x4 b, int sa, int sb)
+{
+    static_assert(OPA >= 0 && OPA < 4 && OPB >= 0 && OPB < 4, "op_sel byte index");
+    asm("s_nop 1\n\t"
+        "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[%5,%6,0] "
+        "op_sel_hi:[%7,%8,0] cbsz:4 blgp:4"
+        : "+a"(acc)
+        : "v"(a), "v"(b), "v"(sa), "v"(sb), "n"(OPA & 1), "n"(OPB & 1), "n"(OPA >> 1),
+          "n"(OPB >> 1));
+}
+
+// Wait states between the last MFMA writing an accumulator and any other
+// instruction reading it (gfx9 requires up to ~19 for a 16-pass XDL op).
+__device__ __forceinline__ void mfma_drain()
+{
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+}
+
+// ----------------------------------------------------------- MBS factor
+// f(b) = 1/(1+b/256) = 256/(256+b), correctly rounded to fp32, computed at
+// compile time with integer long division (no run-time division needed).
+constexpr uint32_t mbs_factor_bits(int b)
+{
+    if (b == 0) return 0x3F800000u;
+    const uint64_t d = 256u + (uint64_t)b;
+    const uint64_t num = 1ull << 32;  // 256 * 2^24: the quotient is the
+    uint64_t q = num / d;             // significand of a value in (0.5, 1)
+    const uint64_t r = num % d;
+    if (2 * r > d || (2 * r == d && (q & 1))) ++q;
+    return (126u << 23) | (uint32_t)(q - (1u << 23));
+}
+struct FactorTable {
+    uint32_t bits[256];
+    constexpr FactorTable() : bits{}
+    {
+        for (int b = 0; b < 256; ++b) bits[b] = mbs_factor_bits(b);
+    }
+};
+
+// ------------------------------------------------------------ bf16 pack
+// Two fp32 -> packed bf16x2, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
+{
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+}  // namespace mbs

@@ -1,0 +1,123 @@
+"""CPU-side checks of the drop-in boundary: the C-ABI library loads and
+exports every function include/mbs_gemm_a4w4.h declares; argument validation
+returns the documented status codes without touching a GPU; the torch module
+raises RuntimeError on bad operands (reference semantics,
+interface/gemm_a4w4_pybind.cpp:22-44); plan selection is pure host logic."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "mbs_gemm_a4w4.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mbs_\w+)\s*\(", text)))
+
+
+def test_header_symbols_exported():
+    import mbs_amd
+
+    lib = mbs_amd.clib()
+    names = header_functions()
+    assert "mbs_gemm_a4w4_launch" in names and len(names) >= 13
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def c_lib():
+    import mbs_amd
+
+    L = mbs_amd.clib()
+    P, I, S = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    L.mbs_gemm_a4w4_launch.argtypes = [P, P, P, P, P, P, P, I, I, I, I, I, P, S, P]
+    L.mbs_gemm_a4w4_launch.restype = I
+    L.mbs_status_string.restype = ctypes.c_char_p
+    L.mbs_last_error.restype = ctypes.c_char_p
+    L.mbs_gemm_a4w4_plan_name.argtypes = [I, I, I, ctypes.c_char_p, S]
+    L.mbs_gemm_a4w4_workspace_bytes.argtypes = [I, I, I]
+    L.mbs_gemm_a4w4_workspace_bytes.restype = S
+    L.mbs_gemm_a4w4_config_name.restype = ctypes.c_char_p
+    return L
+
+
+FAKE = 0x1000  # never dereferenced: validation fails first
+
+
+@pytest.mark.parametrize("M,N,K,Mpad,snp,why", [
+    (0, 256, 512, 32, 16, "M >= 1"),
+    (128, 250, 512, 128, 16, "multiple of 16"),
+    (128, 256, 480, 128, 16, "multiple of 64"),
+    (128, 256, 512, 130, 16, "Mpad"),
+    (128, 256, 512, 128, 17, "scaleN_pad"),
+])
+def test_launch_rejects_bad_shapes(M, N, K, Mpad, snp, why):
+    L = c_lib()
+    st = L.mbs_gemm_a4w4_launch(FAKE, FAKE, FAKE, FAKE, None, None, FAKE, M, N, K, Mpad, snp,
+                                None, 0, None)
+    assert st == 1  # MBS_ERR_ARGUMENT
+    assert why in L.mbs_last_error().decode()
+    assert L.mbs_status_string(st) == b"invalid argument"
+
+
+def test_launch_rejects_null_and_half_factors():
+    L = c_lib()
+    assert L.mbs_gemm_a4w4_launch(None, FAKE, FAKE, FAKE, None, None, FAKE, 128, 256, 512, 128, 16,
+                                  None, 0, None) == 1
+    assert L.mbs_gemm_a4w4_launch(FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, 128, 256, 512, 128, 16,
+                                  None, 0, None) == 1
+    assert b"together" in L.mbs_last_error()
+
+
+def test_plans_cover_every_config_shape():
+    from mbs_amd import synthetic
+
+    L = c_lib()
+    buf = ctypes.create_string_buffer(256)
+    for cfg in range(5):
+        for (M, N, K) in synthetic.config_shapes(cfg):
+            assert L.mbs_gemm_a4w4_plan_name(M, N, K, buf, 256) == 0
+            name = buf.value.decode()
+            if M <= 32:
+                assert name.startswith("skinny"), (M, N, K, name)
+            else:
+                assert name.startswith("tiled"), (M, N, K, name)
+    L.mbs_gemm_a4w4_plan_name(8192, 8192, 8192, buf, 256)
+    assert buf.value.decode().startswith("tiled_256x256")
+    assert L.mbs_gemm_a4w4_workspace_bytes(8192, 8192, 8192) == 0
+
+
+def test_format_entry_points_validate():
+    L = c_lib()
+    P, I = ctypes.c_void_p, ctypes.c_int
+    L.mbs_shuffle_b.argtypes = [P, P, I, I, P]
+    L.mbs_quantize_mxfp4_bf16.argtypes = [P, I, I, P, P, P, I, P]
+    L.mbs_dequant_mxfp4.argtypes = [P, P, P, I, I, I, P]
+    assert L.mbs_shuffle_b(FAKE, FAKE + 64, 24, 512, None) == 1      # N % 16
+    assert L.mbs_shuffle_b(FAKE, FAKE, 32, 512, None) == 1           # in place
+    assert L.mbs_quantize_mxfp4_bf16(FAKE, 4, 48, FAKE, None, None, 127, None) == 1
+    assert L.mbs_quantize_mxfp4_bf16(FAKE, 4, 64, FAKE, None, None, 300, None) == 1
+    assert L.mbs_dequant_mxfp4(FAKE, FAKE, FAKE, 8, 64, 1, None) == 1  # rows % 16 for B
+
+
+def test_torch_module_rejects_host_tensors_and_bad_shapes():
+    import torch
+
+    import mbs_amd
+
+    m = mbs_amd.ext()
+    A = torch.zeros(128, 256, dtype=torch.uint8)
+    B = torch.zeros(256, 256, dtype=torch.uint8)
+    s = torch.zeros(256 * 16, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="on device"):
+        m.gemm_a4w4(A, B, s, s)
+    with pytest.raises(RuntimeError, match="on device"):
+        m.gemm_a4w4(A, B, s, s, torch.zeros(128, 1, dtype=torch.uint8), torch.zeros(256, 1, dtype=torch.uint8))
+    with pytest.raises(RuntimeError):
+        m.quantize_mxfp4(torch.zeros(4, 64, dtype=torch.bfloat16))
+    assert m.num_configs() >= 8
+    assert m.config_name(0).startswith("tiled")
+    assert "skinny" in m.plan_name(1, 8192, 8192)
