@@ -13,7 +13,7 @@
 // a caller needs nothing beyond this module to prepare operands.
 #include <torch/extension.h>
 
-#include <c10/hip/HIPGuard.h>
+#include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 
 #include <string>
@@ -99,7 +99,7 @@ Operands prepare(const at::Tensor& A, const at::Tensor& B, const at::Tensor& A_s
 
 at::Tensor run(const Operands& o, int config, int splits)
 {
-    c10::hip::HIPGuard guard(o.A.device());
+    c10::DeviceGuard guard(o.A.device());
     auto out = torch::empty({o.Mpad, o.N},
                             torch::TensorOptions().dtype(torch::kBFloat16).device(o.A.device()));
     const size_t ws = config < 0 ? mbs_gemm_a4w4_workspace_bytes(o.M, o.N, o.K)
@@ -155,7 +155,7 @@ std::tuple<at::Tensor, at::Tensor> quantize_mxfp4(at::Tensor x, bool shuffle, in
     auto xc = x.contiguous();
     const int64_t R = xc.size(0), K = xc.size(1);
     TORCH_CHECK(K % 32 == 0, "quantize_mxfp4: K must be a multiple of 32");
-    c10::hip::HIPGuard guard(x.device());
+    c10::DeviceGuard guard(x.device());
     auto opts = torch::TensorOptions().dtype(torch::kByte).device(x.device());
     auto packed = torch::empty({R, K / 2}, opts);
     at::Tensor scales = shuffle ? torch::empty({round_up(R, 32), scale_pad(K)}, opts)
@@ -174,7 +174,7 @@ at::Tensor shuffle_weight(at::Tensor w)
     TORCH_CHECK(w.is_cuda() && w.dim() == 2 && w.element_size() == 1,
                 "shuffle_weight: w must be a 2D 1-byte device tensor");
     auto wu = as_bytes(w);
-    c10::hip::HIPGuard guard(w.device());
+    c10::DeviceGuard guard(w.device());
     auto out = torch::empty_like(wu);
     check_status(mbs_shuffle_b(wu.data_ptr<uint8_t>(), out.data_ptr<uint8_t>(), (int)wu.size(0),
                                (int)(wu.size(1) * 2), current_stream(w)),
@@ -189,7 +189,7 @@ at::Tensor shuffle_scales(at::Tensor s, int64_t pad_byte)
                 "shuffle_scales: s must be a 2D 1-byte device tensor");
     auto su = as_bytes(s);
     const int64_t R = su.size(0), K = su.size(1) * 32;
-    c10::hip::HIPGuard guard(s.device());
+    c10::DeviceGuard guard(s.device());
     auto out = torch::empty({round_up(R, 32), scale_pad(K)},
                             torch::TensorOptions().dtype(torch::kByte).device(s.device()));
     check_status(mbs_shuffle_scales(su.data_ptr<uint8_t>(), out.data_ptr<uint8_t>(), (int)R, (int)K,
@@ -209,7 +209,7 @@ at::Tensor dequant_mxfp4(at::Tensor packed, at::Tensor scale_shuffled, bool b_pr
     auto su = as_bytes(scale_shuffled);
     const int64_t R = pu.size(0), K = pu.size(1) * 2;
     TORCH_CHECK(su.numel() >= round_up(R, 32) * scale_pad(K), "dequant_mxfp4: scale buffer too small");
-    c10::hip::HIPGuard guard(packed.device());
+    c10::DeviceGuard guard(packed.device());
     auto out = torch::empty({R, K}, torch::TensorOptions().dtype(torch::kFloat32).device(packed.device()));
     check_status(mbs_dequant_mxfp4(pu.data_ptr<uint8_t>(), su.data_ptr<uint8_t>(),
                                    out.data_ptr<float>(), (int)R, (int)K, b_preshuffled ? 1 : 0,
