@@ -142,7 +142,20 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-decode", action="store_true", help="skip the decode shapes")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run 20 device-to-device copies of MIB MiB (scales the HBM "
+                         "FETCH_SIZE/WRITE_SIZE counters) and exit")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        import torch
+
+        a = torch.ones(args.calibrate_copy << 20, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(20):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": a.numel(), "copies": 20}))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures a single MI355X; the MXFP4 GEMM is a one-GPU "
               "kernel here (multi-GPU sharding is described in DESIGN.md, not run). "

@@ -349,6 +349,300 @@ __global__ void __launch_bounds__(T::NT) gemm_tiled_kernel(const GemmArgs p)
 }
 
 // ======================================================================
+// B-direct tiled kernel
+// ======================================================================
+// Same workgroup tiling as gemm_tiled_kernel, but only A goes through LDS:
+// the preshuffled B is already in MFMA fragment order (one 1-KiB
+// contiguous block per 16 rows x 128 K), so each wave loads its B fragments
+// with plain 16-byte buffer loads straight into VGPRs, three stages ahead,
+// into a 4-deep register ring.  Scale dwords (one per lane per 32-row group
+// and 256-K group) are likewise loaded straight into VGPRs.  This halves the
+// LDS traffic of the stage (LDS bandwidth, not the MFMA pipe, is what limits
+// the all-LDS design), and A fragments are read from LDS just in time, two
+// MFMA rows ahead.  The epilogue turns each pair of 16-column fragments into
+// 16-byte row segments with two rounds of permlane swaps before storing.
+template <int BM_, int BN_, int WGM_, int WGN_>
+struct BdShape {
+    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
+    static constexpr int NW = WGM * WGN, NT = 64 * NW;
+    static constexpr int WM = BM / WGM, WN = BN / WGN;
+    static constexpr int FM = WM / 16, FN = WN / 16;
+    static constexpr int AF = BM / 16;                  // A fragments per stage
+    static constexpr int DA = AF / NW;                  // A DMAs per wave per stage
+    static constexpr int SA = FM / 2, SB = FN / 2;      // scale dwords per wave per group
+    static constexpr int ASLOT = AF * 1024;             // bytes of one A ring slot
+    static_assert(AF % NW == 0, "A fragments must split evenly over waves");
+    static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
+    static_assert(4 * ASLOT <= 160 * 1024, "LDS budget");
+};
+
+template <class T, bool KTAIL, bool SPLIT>
+__global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
+{
+    __shared__ __attribute__((aligned(1024))) uint8_t sa0[T::ASLOT];
+    __shared__ __attribute__((aligned(1024))) uint8_t sa1[T::ASLOT];
+    __shared__ __attribute__((aligned(1024))) uint8_t sa2[T::ASLOT];
+    __shared__ __attribute__((aligned(1024))) uint8_t sa3[T::ASLOT];
+    auto aslot = [&](auto B) __attribute__((always_inline)) -> uint8_t* {
+        constexpr int b = decltype(B)::value & 3;
+        if constexpr (b == 0) return sa0;
+        else if constexpr (b == 1) return sa1;
+        else if constexpr (b == 2) return sa2;
+        else return sa3;
+    };
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = w / T::WGN, wn = w % T::WGN;
+
+    int bid = blockIdx.x;
+    const int G = gridDim.x;
+    if ((G & 7) == 0) bid = (bid & 7) * (G >> 3) + (bid >> 3);
+    const int tiles = p.tiles_m * p.tiles_n;
+    const int split = bid / tiles;
+    const int t = bid - split * tiles;
+    constexpr int GROUP = 8;
+    const int grp = t / (GROUP * p.tiles_n);
+    const int first_m = grp * GROUP;
+    const int gsz = min(p.tiles_m - first_m, GROUP);
+    const int tin = t - grp * GROUP * p.tiles_n;
+    const int m0 = (first_m + tin % gsz) * T::BM;
+    const int n0 = (tin / gsz) * T::BN;
+
+    const int K = p.K, Kp = K >> 1;
+    const int S_total = (K + 127) >> 7;
+    const int s_begin = split * p.sps;
+    const int n_st = min(p.sps, S_total - s_begin);
+
+    const int rows_a = min(T::BM, p.M - m0);
+    const int rows_b = min(T::BN, p.N - n0);
+    const int Mpad = (p.M + 31) & ~31, Npad = (p.N + 31) & ~31;
+    const rsrc_t rA = make_rsrc(p.A + (size_t)m0 * Kp, (uint32_t)(rows_a * Kp));
+    const rsrc_t rB = make_rsrc(p.B + (size_t)(n0 >> 4) * K * 8, (uint32_t)(rows_b * Kp));
+    const rsrc_t rAs = make_rsrc(p.As + (size_t)(m0 >> 5) * 32 * p.snp,
+                                 (uint32_t)(min(T::BM, Mpad - m0) * p.snp));
+    const rsrc_t rBs = make_rsrc(p.Bs + (size_t)(n0 >> 5) * 32 * p.snp,
+                                 (uint32_t)(min(T::BN, Npad - n0) * p.snp));
+
+    // Per-lane offsets are fixed for the whole K loop; the stage offset and
+    // the out-of-range bit go into the scalar offset.
+    // A DMA: fragment f, lane i -> row 16f + i%16, K-block i/16 of the stage.
+    uint32_t voA[T::DA];
+    static_for<T::DA>([&](auto d) {
+        voA[d] = (uint32_t)((16 * (w * T::DA + d) + (lane & 15)) * Kp + (lane >> 4) * 16);
+    });
+    // B: the wave's fragment j is 16 rows at n0 + wn*WN + 16j.
+    uint32_t voB[T::FN];
+    static_for<T::FN>([&](auto j) {
+        voB[j] = (uint32_t)((wn * T::FN + j) * K * 8 + lane * 16);
+    });
+    uint32_t voSA[T::SA], voSB[T::SB];
+    static_for<T::SA>([&](auto i) {
+        voSA[i] = (uint32_t)((((wm * T::WM) >> 5) + i) * 32 * p.snp + lane * 4);
+    });
+    static_for<T::SB>([&](auto j) {
+        voSB[j] = (uint32_t)((((wn * T::WN) >> 5) + j) * 32 * p.snp + lane * 4);
+    });
+    const bool hi_lane = lane >= 32;
+    const uint32_t hi_bit = hi_lane ? kOOB : 0u;
+
+    i32x4 rb[4][T::FN];     // B register ring (stage % 4)
+    i32x4 ra[4];            // A fragment ring (fragment sequence % 4)
+    int sa[2][T::SA], sb[2][T::SB];
+    f32x4 acc[T::FM][T::FN];
+    static_for<T::FM>([&](auto i) {
+        static_for<T::FN>([&](auto j) { acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f}; });
+    });
+
+    // Scalar out-of-range bit of local stage ls (stage past the split end).
+    auto dead_s = [&](int ls) __attribute__((always_inline)) {
+        return (uint32_t)(ls >= n_st) << 31;
+    };
+    // Per-lane out-of-range bit: K-blocks 2,3 of the K-tail stage (KTAIL only).
+    auto tail_v = [&](int ls) __attribute__((always_inline)) {
+        uint32_t t = ((uint32_t)(s_begin + ls == S_total - 1) << 31) & hi_bit;
+        asm volatile("" : "+v"(t));
+        return t;
+    };
+    // VMEM items issued at local stage ls (static slot u = ls & 3):
+    //   DA A-DMAs and FN B-loads for stage ls+3, and (u even) the SA+SB scale
+    //   dwords of 256-K group (ls+2)/2.
+    auto issue_item = [&](auto U, auto D, int ls) __attribute__((always_inline)) {
+        constexpr int u = decltype(U)::value;
+        constexpr int d = decltype(D)::value;
+        if constexpr (d < T::DA + T::FN) {
+            const int s = s_begin + ls + 3;
+            const uint32_t tv = KTAIL ? tail_v(ls + 3) : 0u;
+            if constexpr (d < T::DA) {
+                dma16s(rA, aslot(std::integral_constant<int, u + 3>{}) + (w * T::DA + d) * 1024,
+                       voA[d] | tv, ((uint32_t)s * 64u) | dead_s(ls + 3));
+            } else {
+                constexpr int j = d - T::DA;
+                rb[(u + 3) & 3][j] = load16s(rB, voB[j] | tv, ((uint32_t)s * 1024u) | dead_s(ls + 3));
+            }
+        } else {
+            constexpr int e = d - T::DA - T::FN;
+            constexpr int set = ((u + 2) >> 1) & 1;
+            const uint32_t so = (uint32_t)((s_begin + ls + 2) >> 1) * 256u | dead_s(ls + 2);
+            if constexpr (e < T::SA)
+                sa[set][e] = load4s(rAs, voSA[e], so);
+            else
+                sb[set][e - T::SA] = load4s(rBs, voSB[e - T::SA], so);
+        }
+    };
+    constexpr int NI_ODD = T::DA + T::FN;
+    constexpr int NI_EVEN = T::DA + T::FN + T::SA + T::SB;
+
+    // A fragment x of the stage in ring slot BUF -> register ra[R].
+    auto read_a = [&](auto BUF, auto X, auto R) __attribute__((always_inline)) {
+        ra[decltype(R)::value] = *reinterpret_cast<const i32x4*>(
+            aslot(BUF) + (wm * T::FM + decltype(X)::value) * 1024 + lane * 16);
+    };
+
+    auto stage = [&](auto U, int ls) __attribute__((always_inline)) {
+        constexpr int u = decltype(U)::value;
+        constexpr int h = u & 1, sset = (u >> 1) & 1;
+        constexpr int NI = ((u & 1) == 0) ? NI_EVEN : NI_ODD;   // issues of this stage
+        constexpr int NIP = ((u & 1) == 0) ? NI_ODD : NI_EVEN;  // issues of the previous one
+        constexpr int NCH = T::FM;
+        // Everything issued two or more stages ago has landed (A of ls+1 for
+        // this stage's look-ahead reads, B and scales of ls); the previous
+        // stage's issues may still be in flight.
+        wait_vmcnt<NIP>();
+        barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        int sav[T::SA], sbv[T::SB];
+        static_for<T::SA>([&](auto i) { sav[i] = sa[sset][i]; });
+        static_for<T::SB>([&](auto j) { sbv[j] = sb[sset][j]; });
+        if constexpr (KTAIL) {
+            const bool tail = (s_begin + ls == S_total - 1) && hi_lane;
+            static_for<T::SA>([&](auto i) { sav[i] = tail ? 0x7F7F7F7F : sav[i]; });
+            static_for<T::SB>([&](auto j) { sbv[j] = tail ? 0x7F7F7F7F : sbv[j]; });
+        }
+        static_for<NCH>([&](auto C) {
+            constexpr int c = decltype(C)::value;
+            // look-ahead A read: fragment c+2 of this stage or of the next
+            constexpr int xn = c + 2;
+            if constexpr (xn < T::FM)
+                read_a(std::integral_constant<int, u>{}, std::integral_constant<int, xn>{},
+                       std::integral_constant<int, (T::FM * u + xn) & 3>{});
+            else
+                read_a(std::integral_constant<int, u + 1>{},
+                       std::integral_constant<int, xn - T::FM>{},
+                       std::integral_constant<int, (T::FM * u + xn) & 3>{});
+            static_for<NI>([&](auto D) {
+                if constexpr (D * NCH / NI == c) issue_item(U, D, ls);
+            });
+            constexpr int ar = (T::FM * u + c) & 3;
+            static_for<T::FN>([&](auto j) {
+                constexpr int opb = (j & 1) + 2 * h;
+                constexpr int opa = (c & 1) + 2 * h;
+                mfma_fp4<opb, opa>(acc[c][j], rb[u][j], ra[ar], sbv[j / 2], sav[c / 2]);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+
+    // ---- prologue: issue stages 0..2 (A, B) and scale group 0 ------------
+    static_for<3>([&](auto P) {
+        constexpr int ps = decltype(P)::value;
+        const int s = s_begin + ps;
+        const uint32_t tv = KTAIL ? tail_v(ps) : 0u;
+        static_for<T::DA>([&](auto d) {
+            dma16s(rA, aslot(P) + (w * T::DA + d) * 1024, voA[d] | tv,
+                   ((uint32_t)s * 64u) | dead_s(ps));
+        });
+        static_for<T::FN>([&](auto j) {
+            rb[ps][j] = load16s(rB, voB[j] | tv, ((uint32_t)s * 1024u) | dead_s(ps));
+        });
+        if constexpr (ps == 0) {  // scale group 0 (stages 0, 1)
+            const uint32_t so = (uint32_t)(s_begin >> 1) * 256u;
+            static_for<T::SA>([&](auto i) { sa[0][i] = load4s(rAs, voSA[i], so); });
+            static_for<T::SB>([&](auto j) { sb[0][j] = load4s(rBs, voSB[j], so); });
+        }
+    });
+    // The first stage is issued like stage "-2" and "-1" would be: wait for
+    // everything except stage 2's group, then read A fragments 0 and 1.
+    wait_vmcnt<T::DA + T::FN>();
+    barrier();
+    read_a(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{},
+           std::integral_constant<int, 0>{});
+    read_a(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{},
+           std::integral_constant<int, 1>{});
+
+    // ---- main loop (stage count padded to a multiple of 4 with zero stages)
+    const int n_st4 = (n_st + 3) & ~3;
+    for (int ls0 = 0; ls0 < n_st4; ls0 += 4) {
+        static_for<4>([&](auto U) { stage(U, ls0 + decltype(U)::value); });
+    }
+    wait_vmcnt<0>();
+    mfma_drain();
+
+    // ---- epilogue ----------------------------------------------------------
+    const bool has_f = (p.Af != nullptr) && (p.Bf != nullptr);
+    const int row_l = wm * T::WM + (lane & 15);
+    const int col_w = n0 + wn * T::WN;
+    const int q = lane >> 4;
+    if constexpr (SPLIT) {
+        const rsrc_t rW = make_rsrc(p.ws + ((size_t)split * p.M + m0) * p.N,
+                                    (uint32_t)(rows_a * p.N * 4));
+        static_for<T::FN>([&](auto j) {
+            const int c = col_w + j * 16;
+            if (c < p.N) {
+                static_for<T::FM>([&](auto i) {
+                    store16(rW, (uint32_t)(((row_l + i * 16) * p.N + c + q * 4) * 4), acc[i][j]);
+                });
+            }
+        });
+    } else {
+        const rsrc_t rAf = make_rsrc(p.Af + m0, has_f ? (uint32_t)rows_a : 0u);
+        const rsrc_t rBf = make_rsrc(p.Bf, has_f ? (uint32_t)p.N : 0u);
+        const rsrc_t rO = make_rsrc(p.out + (size_t)m0 * p.N, (uint32_t)(rows_a * p.N * 2));
+        float fa[T::FM];
+        static_for<T::FM>([&](auto i) {
+            fa[i] = has_f ? factor_of(load1(rAf, row_l + i * 16)) : 1.0f;
+        });
+        // Fragment pair (2p, 2p+1) covers 32 columns.  Lane (m, q) holds
+        // columns 4q..4q+3 of each; after the swaps it holds 8 consecutive
+        // columns 8q..8q+7 of the pair: a 16-byte store.
+        static_for<T::FN / 2>([&](auto P2) {
+            constexpr int j0 = 2 * decltype(P2)::value;
+            const int c = col_w + j0 * 16;
+            if (c < p.N) {  // N % 16 == 0: the pair is all in or only its first half
+                const uint32_t b0 = (uint32_t)load4(rBf, c + q * 4);
+                const uint32_t b1 = (uint32_t)load4(rBf, c + 16 + q * 4);
+                float f0[4], f1[4];
+                for (int k = 0; k < 4; ++k) {
+                    f0[k] = has_f ? factor_of(b0 >> (8 * k)) : 1.0f;
+                    f1[k] = has_f ? factor_of(b1 >> (8 * k)) : 1.0f;
+                }
+                const bool second_ok = c + 16 < p.N;
+                static_for<T::FM>([&](auto i) {
+                    f32x4 v0 = acc[i][j0], v1 = acc[i][j0 + 1];
+                    for (int k = 0; k < 4; ++k) {
+                        v0[k] = v0[k] * (fa[i] * f0[k]);
+                        v1[k] = v1[k] * (fa[i] * f1[k]);
+                    }
+                    uint32_t x0 = pack_bf16x2(v0[0], v0[1]), x1 = pack_bf16x2(v0[2], v0[3]);
+                    uint32_t y0 = pack_bf16x2(v1[0], v1[1]), y1 = pack_bf16x2(v1[2], v1[3]);
+                    // round A: upper half of x <-> lower half of y
+                    auto a0 = __builtin_amdgcn_permlane32_swap(x0, y0, false, false);
+                    auto a1 = __builtin_amdgcn_permlane32_swap(x1, y1, false, false);
+                    // round B: odd rows of x <-> even rows of y
+                    auto b0s = __builtin_amdgcn_permlane16_swap(a0[0], a0[1], false, false);
+                    auto b1s = __builtin_amdgcn_permlane16_swap(a1[0], a1[1], false, false);
+                    const uint32_t o = (uint32_t)(((row_l + i * 16) * p.N + c + q * 8) * 2);
+                    if (second_ok || q < 2) {
+                        i32x4 v = {(int)b0s[0], (int)b1s[0], (int)b0s[1], (int)b1s[1]};
+                        store16(rO, o, __builtin_bit_cast(f32x4, v));
+                    }
+                });
+            }
+        });
+    }
+}
+
+// ======================================================================
 // Skinny (decode) kernel: M <= 16*MT, MT in {1,2}
 // ======================================================================
 template <int MT, int NWK, int U, bool SPLIT>
@@ -509,6 +803,19 @@ hipError_t launch_tiled(const GemmArgs& a, dim3 grid, bool ktail, bool split, hi
     return hipGetLastError();
 }
 
+template <class T>
+hipError_t launch_bdirect(const GemmArgs& a, dim3 grid, bool ktail, bool split, hipStream_t s)
+{
+    if (ktail) {
+        if (split) hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, true>), grid, dim3(T::NT), 0, s, a);
+        else hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false>), grid, dim3(T::NT), 0, s, a);
+    } else {
+        if (split) hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, true>), grid, dim3(T::NT), 0, s, a);
+        else hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false>), grid, dim3(T::NT), 0, s, a);
+    }
+    return hipGetLastError();
+}
+
 template <int MT, int NWK, int U>
 hipError_t launch_skinny(const GemmArgs& a, dim3 grid, bool, bool split, hipStream_t s)
 {
@@ -525,6 +832,14 @@ using T64x256 = TileShape<64, 256, 1, 4>;
 using T64x128 = TileShape<64, 128, 1, 2>;
 using T64x64 = TileShape<64, 64, 1, 1>;
 
+using B256x256 = BdShape<256, 256, 2, 2>;
+using B256x128 = BdShape<256, 128, 2, 2>;
+using B128x256 = BdShape<128, 256, 2, 2>;
+using B128x128 = BdShape<128, 128, 2, 2>;
+using B64x256 = BdShape<64, 256, 1, 4>;
+using B64x128 = BdShape<64, 128, 1, 2>;
+using B64x64 = BdShape<64, 64, 1, 1>;
+
 const Config kConfigs[] = {
     {"tiled_256x256_w2x2", kTiled, 256, 256, 256, 1, 1.00f, launch_tiled<T256x256>},
     {"tiled_256x128_w2x2", kTiled, 256, 128, 256, 1, 0.85f, launch_tiled<T256x128>},
@@ -533,6 +848,13 @@ const Config kConfigs[] = {
     {"tiled_64x256_w1x4", kTiled, 64, 256, 256, 2, 0.65f, launch_tiled<T64x256>},
     {"tiled_64x128_w1x2", kTiled, 64, 128, 128, 3, 0.50f, launch_tiled<T64x128>},
     {"tiled_64x64_w1x1", kTiled, 64, 64, 64, 4, 0.35f, launch_tiled<T64x64>},
+    {"bdirect_256x256_w2x2", kTiled, 256, 256, 256, 1, 1.10f, launch_bdirect<B256x256>},
+    {"bdirect_256x128_w2x2", kTiled, 256, 128, 256, 1, 0.95f, launch_bdirect<B256x128>},
+    {"bdirect_128x256_w2x2", kTiled, 128, 256, 256, 1, 0.95f, launch_bdirect<B128x256>},
+    {"bdirect_128x128_w2x2", kTiled, 128, 128, 256, 2, 0.78f, launch_bdirect<B128x128>},
+    {"bdirect_64x256_w1x4", kTiled, 64, 256, 256, 2, 0.72f, launch_bdirect<B64x256>},
+    {"bdirect_64x128_w1x2", kTiled, 64, 128, 128, 3, 0.56f, launch_bdirect<B64x128>},
+    {"bdirect_64x64_w1x1", kTiled, 64, 64, 64, 4, 0.40f, launch_bdirect<B64x64>},
     {"skinny_m16_k8", kSkinny, 16, 32, 1024, 1, 1.0f, launch_skinny<1, 8, 8>},
     {"skinny_m32_k8", kSkinny, 32, 32, 1024, 1, 1.0f, launch_skinny<2, 8, 8>},
     {"skinny_m16_k4", kSkinny, 16, 32, 512, 2, 1.0f, launch_skinny<1, 4, 8>},

@@ -61,6 +61,22 @@ __device__ __forceinline__ void dma4(rsrc_t r, void* lds, uint32_t voffset)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, MBS_LDS_PTR(lds), 4, voffset, 0, 0, 0);
 }
 
+// Variants with a wave-uniform scalar offset: the range check covers
+// voffset + soffset (checked on gfx950), so per-stage offsets and the
+// out-of-range bit can live in an SGPR and cost no VALU work.
+__device__ __forceinline__ void dma16s(rsrc_t r, void* lds, uint32_t voffset, uint32_t soffset)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, MBS_LDS_PTR(lds), 16, voffset, soffset, 0, 0);
+}
+__device__ __forceinline__ i32x4 load16s(rsrc_t r, uint32_t voffset, uint32_t soffset)
+{
+    return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0));
+}
+__device__ __forceinline__ int load4s(rsrc_t r, uint32_t voffset, uint32_t soffset)
+{
+    return (int)__builtin_amdgcn_raw_buffer_load_b32(r, voffset, soffset, 0);
+}
+
 __device__ __forceinline__ i32x4 load16(rsrc_t r, uint32_t voffset)
 {
     return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 0));
