@@ -84,9 +84,9 @@ def test_plans_cover_every_config_shape():
             if M <= 32:
                 assert name.startswith("skinny"), (M, N, K, name)
             else:
-                assert name.startswith("tiled"), (M, N, K, name)
+                assert name.split("_")[0] in ("tiled", "bdirect"), (M, N, K, name)
     L.mbs_gemm_a4w4_plan_name(8192, 8192, 8192, buf, 256)
-    assert buf.value.decode().startswith("tiled_256x256")
+    assert "_256x256_" in buf.value.decode()
     assert L.mbs_gemm_a4w4_workspace_bytes(8192, 8192, 8192) == 0
 
 
