@@ -109,7 +109,7 @@ def decode_bench(dev, Ms=(1, 4, 16, 32), N=8192, K=8192, copies=10, replays=20):
     return res
 
 
-def cpu_baseline(x, w, rows=2048, reps=3):
+def cpu_baseline(x, w, rows=8192, reps=3):
     """The oracle's run_torch restatement (dequant to fp32, torch.mm fp32,
     bf16) on this host: `rows` rows of the config-1 A against the full W."""
     import torch
