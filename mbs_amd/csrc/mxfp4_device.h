@@ -68,6 +68,10 @@ __device__ __forceinline__ void dma16s(rsrc_t r, void* lds, uint32_t voffset, ui
 {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, MBS_LDS_PTR(lds), 16, voffset, soffset, 0, 0);
 }
+__device__ __forceinline__ void dma4s(rsrc_t r, void* lds, uint32_t voffset, uint32_t soffset)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, MBS_LDS_PTR(lds), 4, voffset, soffset, 0, 0);
+}
 __device__ __forceinline__ i32x4 load16s(rsrc_t r, uint32_t voffset, uint32_t soffset)
 {
     return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0));
@@ -80,6 +84,12 @@ __device__ __forceinline__ int load4s(rsrc_t r, uint32_t voffset, uint32_t soffs
 __device__ __forceinline__ i32x4 load16(rsrc_t r, uint32_t voffset)
 {
     return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 0));
+}
+// Non-temporal 16-byte load (cache-policy bit 1, "nt" on gfx950): for data
+// read exactly once, such as the weight stream of a decode GEMM.
+__device__ __forceinline__ i32x4 load16nt(rsrc_t r, uint32_t voffset)
+{
+    return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 2));
 }
 __device__ __forceinline__ int load4(rsrc_t r, uint32_t voffset)
 {
@@ -138,21 +148,43 @@ __device__ __forceinline__ void barrier()
 // Written as inline asm with the accumulator tied to an AGPR ("+a") so every
 // MFMA accumulates in place: with the builtin the register allocator renames
 // accumulators across the unrolled K loop and emits a v_accvgpr copy per MFMA.
-// Because the compiler's hazard recognizer cannot see into the asm, each MFMA
-// starts with s_nop 1: the two wait states gfx9 needs between a VALU write of
-// a VGPR and an MFMA reading it.  (Loads need none: their results are waited
-// for with s_waitcnt.)  Reading the accumulators after the last MFMA needs the
-// wait of mfma_drain().
+// Because the compiler's hazard recognizer cannot see into the asm, an MFMA
+// whose operands may come from a VALU instruction starts with s_nop 1: the two
+// wait states gfx9 needs between a VALU write of a VGPR and an MFMA reading it.
+// NOP = false is for loops where every operand comes straight from a buffer or
+// LDS load (waited for with s_waitcnt), so no VALU write precedes the MFMA.
+// Reading the accumulators after the last MFMA needs the wait of mfma_drain().
+// First MFMA of an accumulation: C = 0 (inline constant), so the
+// accumulator needs no zeroing and is only written.
 template <int OPA, int OPB>
+__device__ __forceinline__ void mfma_fp4_first(f32x4& acc, i32x4 a, i32x4 b, int sa, int sb)
+{
+    static_assert(OPA >= 0 && OPA < 4 && OPB >= 0 && OPB < 4, "op_sel byte index");
+    asm("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, 0, %3, %4 op_sel:[%5,%6,0] "
+        "op_sel_hi:[%7,%8,0] cbsz:4 blgp:4"
+        : "=a"(acc)
+        : "v"(a), "v"(b), "v"(sa), "v"(sb), "n"(OPA & 1), "n"(OPB & 1), "n"(OPA >> 1),
+          "n"(OPB >> 1));
+}
+
+template <int OPA, int OPB, bool NOP = true>
 __device__ __forceinline__ void mfma_fp4(f32x4& acc, i32x4 a, i32x4 b, int sa, int sb)
 {
     static_assert(OPA >= 0 && OPA < 4 && OPB >= 0 && OPB < 4, "op_sel byte index");
-    asm("s_nop 1\n\t"
-        "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[%5,%6,0] "
-        "op_sel_hi:[%7,%8,0] cbsz:4 blgp:4"
-        : "+a"(acc)
-        : "v"(a), "v"(b), "v"(sa), "v"(sb), "n"(OPA & 1), "n"(OPB & 1), "n"(OPA >> 1),
-          "n"(OPB >> 1));
+    if constexpr (NOP) {
+        asm("s_nop 1\n\t"
+            "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[%5,%6,0] "
+            "op_sel_hi:[%7,%8,0] cbsz:4 blgp:4"
+            : "+a"(acc)
+            : "v"(a), "v"(b), "v"(sa), "v"(sb), "n"(OPA & 1), "n"(OPB & 1), "n"(OPA >> 1),
+              "n"(OPB >> 1));
+    } else {
+        asm("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[%5,%6,0] "
+            "op_sel_hi:[%7,%8,0] cbsz:4 blgp:4"
+            : "+a"(acc)
+            : "v"(a), "v"(b), "v"(sa), "v"(sb), "n"(OPA & 1), "n"(OPB & 1), "n"(OPA >> 1),
+              "n"(OPB >> 1));
+    }
 }
 
 // Wait states between the last MFMA writing an accumulator and any other

@@ -1,0 +1,157 @@
+#!/usr/bin/env python3
+"""Side-by-side GPU timing of this library's GEMM and the reference's own
+kernel (built from its sources into oracle/_ref/libref_gemm.so by
+oracle/Makefile), on identical operand bytes.  Test infrastructure: run by
+hand on a GPU box, not collected by pytest.
+
+    python tests/compare_ref_kernel.py [--replays 20]
+
+For every shape both launchers get the same A, B, scales (and factors where
+the reference's workgroup path needs them: kernel/gemm_a4w4.hip:1044-1146
+takes its factor pointers unconditionally there), the outputs are compared
+against each other with the north-star tolerance, and each launcher is timed
+by HIP-graph replay (one graph of `copies` launches, replayed `replays`
+times).  Decode shapes rotate ten weight copies (cold: more bytes than the
+MALL); large shapes reuse one copy, as the reference's own measurement does
+(asm_vs_wg_kernel.md:179-180).  Prints one JSON object per shape.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+sys.path.insert(0, ROOT)
+sys.path.insert(0, HERE)
+
+REF = os.path.join(ROOT, "oracle", "_ref", "libref_gemm.so")
+SYM = "_Z22gemm_a4w4_mxfp4_launchPKhS0_S0_S0_S0_S0_PviiiiiS1_"
+
+# (M, N, K, factors): the reference's published shapes (asm_vs_wg_kernel.md:191-196),
+# the headline 8192^3, and the decode slice (single-wave path: no factors).
+SHAPES = [
+    (8192, 8192, 8192, True),
+    (8192, 17408, 5120, True),
+    (8192, 5120, 17408, True),
+    (8192, 10240, 5120, True),
+    (8192, 12288, 5120, True),
+    (1024, 17408, 5120, True),
+    (1024, 1024, 5120, True),
+    (1, 8192, 8192, False),
+    (4, 8192, 8192, False),
+    (16, 8192, 8192, False),
+    (32, 8192, 8192, False),
+]
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--replays", type=int, default=20)
+    ap.add_argument("--only", type=str, default="", help="comma list of MxNxK to run")
+    args = ap.parse_args()
+
+    import torch
+
+    import mbs_amd
+    from gpu_util import assert_close, bf16_to_f32, clib
+
+    if not os.path.exists(REF):
+        sys.exit("reference kernel library not built: " + REF)
+    P, I = ctypes.c_void_p, ctypes.c_int
+    ref = getattr(ctypes.CDLL(REF), SYM)
+    ref.argtypes = [P, P, P, P, P, P, P, I, I, I, I, I, P]
+    ref.restype = ctypes.c_bool
+    L = clib()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    only = {s for s in args.only.split(",") if s}
+
+    for M, N, K, factors in SHAPES:
+        if only and f"{M}x{N}x{K}" not in only:
+            continue
+        print(f"[case] {M}x{N}x{K} factors={factors}", file=sys.stderr, flush=True)
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        A, As = mbs_amd.quantize_mxfp4(x, shuffle=True)
+        Wq, Bs = mbs_amd.quantize_mxfp4(w, shuffle=True)
+        B = mbs_amd.shuffle_weight(Wq)
+        del x, w, Wq
+        Mpad = (M + 31) // 32 * 32
+        snp = ((K + 31) // 32 + 7) // 8 * 8
+        cold = M <= 32
+        copies = 10 if cold else 4
+        Bc = [B] + [B.clone() for _ in range(copies - 1)] if cold else [B] * copies
+        Bsc = [Bs] + [Bs.clone() for _ in range(copies - 1)] if cold else [Bs] * copies
+        Af = torch.randint(0, 256, (M,), dtype=torch.uint8, device=dev, generator=g) if factors else None
+        Bf = torch.randint(0, 256, (N,), dtype=torch.uint8, device=dev, generator=g) if factors else None
+        pf = lambda t: None if t is None else P(t.data_ptr())
+        out_ref = torch.zeros(Mpad, N, dtype=torch.bfloat16, device=dev)
+        out_own = torch.zeros(Mpad, N, dtype=torch.bfloat16, device=dev)
+        ws_bytes = L.mbs_gemm_a4w4_workspace_bytes(M, N, K)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+
+        def launch_ref(i):
+            s = P(torch.cuda.current_stream().cuda_stream)
+            return ref(P(A.data_ptr()), P(Bc[i].data_ptr()), P(As.data_ptr()), P(Bsc[i].data_ptr()),
+                       pf(Af), pf(Bf), P(out_ref.data_ptr()), M, N, K, Mpad, snp, s)
+
+        def launch_own(i):
+            s = P(torch.cuda.current_stream().cuda_stream)
+            st = L.mbs_gemm_a4w4_launch(P(A.data_ptr()), P(Bc[i].data_ptr()), P(As.data_ptr()),
+                                        P(Bsc[i].data_ptr()), pf(Af), pf(Bf), P(out_own.data_ptr()),
+                                        M, N, K, Mpad, snp, P(ws.data_ptr()), ws_bytes, s)
+            assert st == 0, L.mbs_last_error()
+            return True
+
+        if not launch_ref(0):
+            print(json.dumps({"shape": [M, N, K], "factors": factors,
+                              "reference": "refused (returned false)"}), flush=True)
+            continue
+        launch_own(0)
+        torch.cuda.synchronize()
+        got, want = bf16_to_f32(out_own[:M]), bf16_to_f32(out_ref[:M])
+        ratio = assert_close(got, want, "ours vs reference kernel")
+
+        def graph_time(launch):
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                for i in range(copies):
+                    launch(i)
+            gr.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(args.replays):
+                gr.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e3 / (args.replays * copies)
+
+        t_ref, t_own = graph_time(launch_ref), graph_time(launch_own)
+        # second pair, reversed order, to spread clock drift over both
+        t_own = min(t_own, graph_time(launch_own))
+        t_ref = min(t_ref, graph_time(launch_ref))
+        flops = 2.0 * M * N * K
+        byts = M * K // 2 + N * K // 2 + (M + N) * K // 32 + 2 * M * N
+        buf = ctypes.create_string_buffer(128)
+        mbs_amd.clib().mbs_gemm_a4w4_plan_name(M, N, K, buf, 128)
+        print(json.dumps({
+            "shape": [M, N, K], "factors": factors, "cold": cold,
+            "ref_us": round(t_ref, 2), "own_us": round(t_own, 2),
+            "speedup": round(t_ref / t_own, 3),
+            "ref_TFLOPS": round(flops / t_ref / 1e6, 1), "own_TFLOPS": round(flops / t_own / 1e6, 1),
+            "ref_GBps": round(byts / t_ref / 1e3, 1), "own_GBps": round(byts / t_own / 1e3, 1),
+            "max_err_over_bound": round(ratio, 4), "own_plan": buf.value.decode(),
+        }), flush=True)
+        del A, B, As, Bs, Bc, Bsc, out_ref, out_own, ws
+        torch.cuda.empty_cache()
+
+
+if __name__ == "__main__":
+    main()
