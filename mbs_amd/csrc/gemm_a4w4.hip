@@ -1072,9 +1072,9 @@ const Config kConfigs[] = {
     {"bdirect_64x256_w1x4", kTiled, 64, 256, 256, 2, 0.72f, launch_bdirect<B64x256>, true},
     {"bdirect_64x128_w1x2", kTiled, 64, 128, 128, 3, 0.56f, launch_bdirect<B64x128>, true},
     {"bdirect_64x64_w1x1", kTiled, 64, 64, 64, 4, 0.40f, launch_bdirect<B64x64>, true},
-    {"bdirect_256x256_w1x4", kTiled, 256, 256, 256, 1, 1.00f, launch_bdirect<B256x256w14>, true},
+    {"bdirect_256x256_w1x4", kTiled, 256, 256, 256, 1, 1.13f, launch_bdirect<B256x256w14>, true},
     {"bdirect_256x128_w1x4", kTiled, 256, 128, 256, 1, 0.90f, launch_bdirect<B256x128w14>, true},
-    {"bdirect_128x256_w1x4", kTiled, 128, 256, 256, 1, 0.90f, launch_bdirect<B128x256w14>, true},
+    {"bdirect_128x256_w1x4", kTiled, 128, 256, 256, 1, 0.97f, launch_bdirect<B128x256w14>, true},
     // skinny: bm = rows covered (16*MT), bn = B rows per workgroup (16*NF)
     // eff = streaming efficiency relative to the best variant (cold N=K=8192 timings)
     {"skinny_m16_n32_w16", kSkinny, 16, 32, 1024, 1, 0.95f, launch_skinny<1, 2, 16, 4>},
