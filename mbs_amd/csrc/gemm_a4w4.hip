@@ -369,7 +369,7 @@ struct BdShape {
     static constexpr int WM = BM / WGM, WN = BN / WGN;
     static constexpr int FM = WM / 16, FN = WN / 16;
     static constexpr int AF = BM / 16;                  // A fragments per stage
-    static constexpr int DA = AF / NW;                  // A DMAs per wave per stage
+    static constexpr int DA = (AF + NW - 1) / NW;       // A DMAs per wave per stage
     static constexpr int SA = FM / 2, SB = FN / 2;      // scale dwords per wave per group
     static constexpr int ASLOT = AF * 1024;             // bytes of one A ring slot
     // Scales of a 256-K group: one 256-byte chunk per 32 rows (A) or columns
@@ -378,8 +378,13 @@ struct BdShape {
     static constexpr int NSDA = (CA + 3) / 4, NSDB = (CB + 3) / 4, NSD = NSDA + NSDB;
     static constexpr int NSDW = (NSD + NW - 1) / NW;    // scale DMAs per wave per group
     static constexpr int SBUF = NSD * 1024;             // bytes of one scale buffer
-    static_assert(AF % NW == 0, "A fragments must split evenly over waves");
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
+    // MBS factor bytes of a unit in LDS: A rows at [0, 256), B columns in
+    // NBC chunks of 256 after them.
+    static constexpr int NBC = (BN + 255) / 256;
+    static constexpr int FBW = 256 * (1 + NBC);
+    static_assert(BM <= 256, "one 256-byte chunk of A factor bytes");
+    static_assert(NW == 1 ? NBC == 1 : NW >= 1 + NBC, "one factor DMA per wave");
     static_assert(4 * ASLOT + 2 * SBUF <= 150 * 1024, "LDS budget");
 };
 
@@ -409,7 +414,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     __shared__ __attribute__((aligned(1024))) uint8_t sa3[T::ASLOT];
     // MBS factor bytes of a unit (A rows at [0,256), B columns at [256,512)),
     // double-buffered by unit parity, and the byte -> fp32 factor table.
-    __shared__ __attribute__((aligned(16))) uint8_t fbytes[2][512];
+    __shared__ __attribute__((aligned(16))) uint8_t fbytes[2][T::FBW];
     __shared__ __attribute__((aligned(16))) uint8_t fjunk[1024];  // target of filler DMAs
     // Scale groups, double-buffered by group parity.
     __shared__ __attribute__((aligned(1024))) uint8_t sc0[T::SBUF];
@@ -558,6 +563,17 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         }
         return t;
     };
+    // A fragment w*DA + d of a stage into its ring slot; when AF is not a
+    // multiple of the wave count, the surplus DMAs read out of range into
+    // fjunk, so every wave issues DA of them.
+    auto a_dma = [&](uint8_t* slot, auto D, const auto& t) __attribute__((always_inline)) {
+        constexpr int d = decltype(D)::value;
+        const int f = w * T::DA + d;
+        if (T::AF % T::NW == 0 || f < T::AF)
+            dma16s(rA, slot + f * 1024, voA[d] | t.tv, t.a);
+        else
+            dma16s(rA, fjunk, voA[d], kOOB);
+    };
     // VMEM items issued at local stage ls (static slot u = ls & 3): DA
     // A-DMAs and FN B-loads for stage ls+3 and, on odd stages, the NSDW scale
     // DMAs of 256-K group (ls+3)/2 into buffer ((ls+3)/2) & 1.
@@ -565,8 +581,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         constexpr int u = decltype(U)::value;
         constexpr int d = decltype(D)::value;
         if constexpr (d < T::DA) {
-            dma16s(rA, aslot(std::integral_constant<int, u + 3>{}) + (w * T::DA + d) * 1024,
-                   voA[d] | t3.tv, t3.a);
+            a_dma(aslot(std::integral_constant<int, u + 3>{}), std::integral_constant<int, d>{}, t3);
         } else if constexpr (d < T::DA + T::FN) {
             constexpr int j = d - T::DA;
             rb[(u + 3) & 3][j] = load16s(rB, voB[j] | t3.tv, t3.b);
@@ -672,16 +687,20 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     const int Mdw = p.M & ~3;
     const rsrc_t rAf = make_rsrc(p.Af, has_f ? (uint32_t)Mdw : 0u);
     const rsrc_t rBf = make_rsrc(p.Bf, has_f ? (uint32_t)p.N : 0u);
+    // Wave 0 loads the A bytes, wave NW-1-c the B chunk c (columns 256c..),
+    // every other wave a filler.
     auto factor_dma = [&](const Unit& un, int par) __attribute__((always_inline)) {
         const bool go = has_f && un.valid;
-        const bool wa = w == 0, wb = w == T::NW - 1;
         if constexpr (T::NW == 1) {
             dma4s(rAf, &fbytes[par][0], (uint32_t)(un.m0 + lane * 4), go ? 0u : kOOB);
             dma4s(rBf, &fbytes[par][256], (uint32_t)(un.n0 + lane * 4), go ? 0u : kOOB);
         } else {
-            uint8_t* dst = wa ? &fbytes[par][0] : (wb ? &fbytes[par][256] : fjunk);
+            const bool wa = w == 0;
+            const int c = T::NW - 1 - w;            // B chunk of this wave
+            const bool wb = !wa && c < T::NBC;
+            uint8_t* dst = wa ? &fbytes[par][0] : (wb ? &fbytes[par][256 * (1 + c)] : fjunk);
             const rsrc_t r = wa ? rAf : rBf;
-            const uint32_t off = (uint32_t)((wa ? un.m0 : un.n0) + lane * 4);
+            const uint32_t off = (uint32_t)((wa ? un.m0 : un.n0 + 256 * c) + lane * 4);
             dma4s(r, dst, off, go && (wa || wb) ? 0u : kOOB);
         }
     };
@@ -699,7 +718,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         constexpr int ps = decltype(P)::value;
         const Tgt t = target(ps);
         static_for<T::DA>([&](auto d) {
-            dma16s(rA, aslot(P) + (w * T::DA + d) * 1024, voA[d] | t.tv, t.a);
+            a_dma(aslot(P), d, t);
         });
         static_for<T::FN>([&](auto j) { rb[ps][j] = load16s(rB, voB[j] | t.tv, t.b); });
     });
@@ -998,7 +1017,13 @@ struct Config {
     int bm, bn;        // tiled: workgroup tile; skinny: rows covered (16*MT) x B rows (16*NF)
     int threads;
     int wgs_per_cu;    // resident workgroups per CU (LDS / register bound)
-    float eff;         // relative per-CU throughput of the tile (cost model)
+    // Cost model constants.  Tiled: {us per 128-K stage with one workgroup
+    // on the CU, us per stage with wgs_per_cu of them, us per work unit},
+    // fitted to graph-replayed timings of every config and split count on 22
+    // shapes on MI355X.  Skinny: {streaming efficiency, 0, 0}.
+    struct {
+        float a, b, c;
+    } cost;
     // launch(args, grid, ktail, split, stream)
     hipError_t (*launch)(const GemmArgs&, dim3, bool, bool, hipStream_t);
     bool persistent = false;  // grid capped at the resident slots; workgroups loop over units
@@ -1054,35 +1079,43 @@ using B64x256 = BdShape<64, 256, 1, 4>;
 using B64x128 = BdShape<64, 128, 1, 2>;
 using B64x64 = BdShape<64, 64, 1, 1>;
 using B256x256w14 = BdShape<256, 256, 1, 4>;
+using B192x256w14 = BdShape<192, 256, 1, 4>;
+using B96x256w14 = BdShape<96, 256, 1, 4>;
+using B64x512w14 = BdShape<64, 512, 1, 4>;
+using B128x384w14 = BdShape<128, 384, 1, 4>;
 using B256x128w14 = BdShape<256, 128, 1, 4>;
 using B128x256w14 = BdShape<128, 256, 1, 4>;
 
 const Config kConfigs[] = {
-    {"tiled_256x256_w2x2", kTiled, 256, 256, 256, 1, 1.00f, launch_tiled<T256x256>},
-    {"tiled_256x128_w2x2", kTiled, 256, 128, 256, 1, 0.85f, launch_tiled<T256x128>},
-    {"tiled_128x256_w2x2", kTiled, 128, 256, 256, 1, 0.85f, launch_tiled<T128x256>},
-    {"tiled_128x128_w2x2", kTiled, 128, 128, 256, 2, 0.70f, launch_tiled<T128x128>},
-    {"tiled_64x256_w1x4", kTiled, 64, 256, 256, 2, 0.65f, launch_tiled<T64x256>},
-    {"tiled_64x128_w1x2", kTiled, 64, 128, 128, 3, 0.50f, launch_tiled<T64x128>},
-    {"tiled_64x64_w1x1", kTiled, 64, 64, 64, 4, 0.35f, launch_tiled<T64x64>},
-    {"bdirect_256x256_w2x2", kTiled, 256, 256, 256, 1, 1.10f, launch_bdirect<B256x256>, true},
-    {"bdirect_256x128_w2x2", kTiled, 256, 128, 256, 1, 0.95f, launch_bdirect<B256x128>, true},
-    {"bdirect_128x256_w2x2", kTiled, 128, 256, 256, 1, 0.95f, launch_bdirect<B128x256>, true},
-    {"bdirect_128x128_w2x2", kTiled, 128, 128, 256, 2, 0.78f, launch_bdirect<B128x128>, true},
-    {"bdirect_64x256_w1x4", kTiled, 64, 256, 256, 2, 0.72f, launch_bdirect<B64x256>, true},
-    {"bdirect_64x128_w1x2", kTiled, 64, 128, 128, 3, 0.56f, launch_bdirect<B64x128>, true},
-    {"bdirect_64x64_w1x1", kTiled, 64, 64, 64, 4, 0.40f, launch_bdirect<B64x64>, true},
-    {"bdirect_256x256_w1x4", kTiled, 256, 256, 256, 1, 1.13f, launch_bdirect<B256x256w14>, true},
-    {"bdirect_256x128_w1x4", kTiled, 256, 128, 256, 1, 0.90f, launch_bdirect<B256x128w14>, true},
-    {"bdirect_128x256_w1x4", kTiled, 128, 256, 256, 1, 0.97f, launch_bdirect<B128x256w14>, true},
+    {"tiled_256x256_w2x2", kTiled, 256, 256, 256, 1, {0.703f, 0.703f, 3.99f}, launch_tiled<T256x256>},
+    {"tiled_256x128_w2x2", kTiled, 256, 128, 256, 1, {0.502f, 0.502f, 1.26f}, launch_tiled<T256x128>},
+    {"tiled_128x256_w2x2", kTiled, 128, 256, 256, 1, {0.418f, 0.418f, 1.43f}, launch_tiled<T128x256>},
+    {"tiled_128x128_w2x2", kTiled, 128, 128, 256, 2, {0.282f, 0.503f, 0.58f}, launch_tiled<T128x128>},
+    {"tiled_64x256_w1x4", kTiled, 64, 256, 256, 2, {0.269f, 0.533f, 0.74f}, launch_tiled<T64x256>},
+    {"tiled_64x128_w1x2", kTiled, 64, 128, 128, 3, {0.232f, 0.427f, 0.25f}, launch_tiled<T64x128>},
+    {"tiled_64x64_w1x1", kTiled, 64, 64, 64, 4, {0.237f, 0.444f, 0.17f}, launch_tiled<T64x64>},
+    {"bdirect_256x256_w2x2", kTiled, 256, 256, 256, 1, {0.686f, 0.686f, 2.81f}, launch_bdirect<B256x256>, true},
+    {"bdirect_256x128_w2x2", kTiled, 256, 128, 256, 1, {0.521f, 0.521f, 0.77f}, launch_bdirect<B256x128>, true},
+    {"bdirect_128x256_w2x2", kTiled, 128, 256, 256, 1, {0.447f, 0.447f, 0.94f}, launch_bdirect<B128x256>, true},
+    {"bdirect_128x128_w2x2", kTiled, 128, 128, 256, 2, {0.338f, 0.536f, 0.47f}, launch_bdirect<B128x128>, true},
+    {"bdirect_64x256_w1x4", kTiled, 64, 256, 256, 2, {0.290f, 0.430f, 0.36f}, launch_bdirect<B64x256>, true},
+    {"bdirect_64x128_w1x2", kTiled, 64, 128, 128, 3, {0.243f, 0.395f, 0.15f}, launch_bdirect<B64x128>, true},
+    {"bdirect_64x64_w1x1", kTiled, 64, 64, 64, 4, {0.264f, 0.411f, 0.09f}, launch_bdirect<B64x64>, true},
+    {"bdirect_256x256_w1x4", kTiled, 256, 256, 256, 1, {0.650f, 0.650f, 2.66f}, launch_bdirect<B256x256w14>, true},
+    {"bdirect_256x128_w1x4", kTiled, 256, 128, 256, 1, {0.474f, 0.474f, 0.74f}, launch_bdirect<B256x128w14>, true},
+    {"bdirect_128x256_w1x4", kTiled, 128, 256, 256, 1, {0.394f, 0.394f, 0.92f}, launch_bdirect<B128x256w14>, true},
+    {"bdirect_192x256_w1x4", kTiled, 192, 256, 256, 1, {0.504f, 0.504f, 1.78f}, launch_bdirect<B192x256w14>, true},
+    {"bdirect_96x256_w1x4", kTiled, 96, 256, 256, 1, {0.351f, 0.351f, 0.37f}, launch_bdirect<B96x256w14>, true},
+    {"bdirect_64x512_w1x4", kTiled, 64, 512, 256, 1, {0.419f, 0.419f, 0.71f}, launch_bdirect<B64x512w14>, true},
+    {"bdirect_128x384_w1x4", kTiled, 128, 384, 256, 1, {0.508f, 0.508f, 1.54f}, launch_bdirect<B128x384w14>, true},
     // skinny: bm = rows covered (16*MT), bn = B rows per workgroup (16*NF)
     // eff = streaming efficiency relative to the best variant (cold N=K=8192 timings)
-    {"skinny_m16_n32_w16", kSkinny, 16, 32, 1024, 1, 0.95f, launch_skinny<1, 2, 16, 4>},
-    {"skinny_m32_n32_w16", kSkinny, 32, 32, 1024, 1, 0.94f, launch_skinny<2, 2, 16, 4>},
-    {"skinny_m16_n32_w8", kSkinny, 16, 32, 512, 2, 1.00f, launch_skinny<1, 2, 8, 8>},
-    {"skinny_m32_n32_w8", kSkinny, 32, 32, 512, 2, 1.00f, launch_skinny<2, 2, 8, 4>},
-    {"skinny_m16_n16_w8", kSkinny, 16, 16, 512, 2, 0.92f, launch_skinny<1, 1, 8, 8>},
-    {"skinny_m32_n16_w8", kSkinny, 32, 16, 512, 2, 0.85f, launch_skinny<2, 1, 8, 8>},
+    {"skinny_m16_n32_w16", kSkinny, 16, 32, 1024, 1, {0.95f, 0.f, 0.f}, launch_skinny<1, 2, 16, 4>},
+    {"skinny_m32_n32_w16", kSkinny, 32, 32, 1024, 1, {0.94f, 0.f, 0.f}, launch_skinny<2, 2, 16, 4>},
+    {"skinny_m16_n32_w8", kSkinny, 16, 32, 512, 2, {1.00f, 0.f, 0.f}, launch_skinny<1, 2, 8, 8>},
+    {"skinny_m32_n32_w8", kSkinny, 32, 32, 512, 2, {1.00f, 0.f, 0.f}, launch_skinny<2, 2, 8, 4>},
+    {"skinny_m16_n16_w8", kSkinny, 16, 16, 512, 2, {0.92f, 0.f, 0.f}, launch_skinny<1, 1, 8, 8>},
+    {"skinny_m32_n16_w8", kSkinny, 32, 16, 512, 2, {0.85f, 0.f, 0.f}, launch_skinny<2, 1, 8, 8>},
 };
 constexpr int kNumConfigs = (int)(sizeof(kConfigs) / sizeof(kConfigs[0]));
 constexpr int kNumCUs = 256;
@@ -1108,6 +1141,8 @@ void split_stages(int K, int want, int* sps, int* splits)
     *splits = (S + per - 1) / per;
 }
 
+double plan_cost(const Plan& pl, int M, int N, int K);
+
 bool make_plan(int config, int want_splits, int M, int N, int K, Plan* out)
 {
     if (config < 0 || config >= kNumConfigs) return false;
@@ -1129,14 +1164,23 @@ bool make_plan(int config, int want_splits, int M, int N, int K, Plan* out)
         pl.grid = dim3(wgs, pl.splits, 1);
     } else {
         const int tm = (M + c.bm - 1) / c.bm, tn = (N + c.bn - 1) / c.bn;
-        int want = want_splits;
-        if (want <= 0) {
-            const int slots = kNumCUs * c.wgs_per_cu;
-            want = 1;
-            // split K while the grid fills less than half the resident slots
-            while (tm * tn * want * 2 <= slots && stages_of(K) / (want * 2) >= 4) want *= 2;
+        if (want_splits <= 0) {
+            // the split count the cost model prefers (workspace below 2 GiB)
+            bool have = false;
+            Plan best{};
+            for (int want : {1, 2, 4, 8}) {
+                Plan cand;
+                if (!make_plan(config, want, M, N, K, &cand)) continue;
+                if (cand.ws_bytes >= (1ull << 31)) continue;
+                if (!have || plan_cost(cand, M, N, K) < plan_cost(best, M, N, K)) {
+                    best = cand;
+                    have = true;
+                }
+            }
+            if (have) *out = best;
+            return have;
         }
-        split_stages(K, want, &pl.sps, &pl.splits);
+        split_stages(K, want_splits, &pl.sps, &pl.splits);
         const int units = tm * tn * pl.splits;
         pl.grid = dim3(c.persistent ? std::min(units, kNumCUs * c.wgs_per_cu) : units, 1, 1);
     }
@@ -1145,13 +1189,14 @@ bool make_plan(int config, int want_splits, int M, int N, int K, Plan* out)
     return true;
 }
 
-// Cost model: estimated time in ns.  Per-CU dense fp4 MFMA rate is
-// 4 SIMD x 4096 flop/clk x 2.4 GHz = 39322 flop/ns; a tile's efficiency
-// `eff` scales it.  Workgroups sharing a CU split its rate.  Split-K adds
-// the partial round trip at ~5 TB/s plus one extra dependent launch.
-constexpr double kCuFlopPerNs = 39322.0;
+// Cost model: estimated time of a plan in ns, including the launch.
+// Tiled kernels: rounds x (stages x stage time + per-unit time), where the
+// stage time grows from cost.a (one workgroup per CU) to cost.b (wgs_per_cu
+// of them); split-K adds the fp32 partial round trip (the reduce kernel).
+// The constants were fitted to measured times (log-error least squares).
+constexpr double kLaunchNs = 4690.0;
+constexpr double kSplitBytesPerNs = 2084.0;
 constexpr double kHbmBytesPerNs = 6000.0;
-constexpr double kExtraLaunchNs = 2500.0;
 // A fragments re-read from L2 by every skinny workgroup (measured ~25 TB/s
 // aggregate when they compete with the B stream).
 constexpr double kL2BytesPerNs = 25000.0;
@@ -1159,25 +1204,32 @@ constexpr double kL2BytesPerNs = 25000.0;
 double plan_cost(const Plan& pl, int M, int N, int K)
 {
     const Config& c = kConfigs[pl.config];
-    const double wgs = (double)pl.grid.x * pl.grid.y;
     const double split_ns =
-        pl.splits > 1 ? (double)pl.ws_bytes * 2.0 / 5000.0 + kExtraLaunchNs : 0.0;
+        pl.splits > 1 ? (double)pl.splits * M * N * 4 * 2 / kSplitBytesPerNs + 1000.0 : 0.0;
     const double hbm_ns =
         ((double)M * K / 2 + (double)N * K / 2 + (double)(M + N) * K / 32 + 2.0 * M * N) /
         kHbmBytesPerNs;
     if (c.family == kSkinny) {
         // bandwidth-bound: needs ~8 waves streaming B per CU to saturate HBM
+        const double wgs = (double)pl.grid.x * pl.grid.y;
         const double waves = wgs * (c.threads / 64);
         const double occ = std::min(1.0, waves / (kNumCUs * 8.0));
         const double a_ns = (double)pl.grid.x * c.bm * (K / 2) / kL2BytesPerNs;
-        return hbm_ns / (std::max(occ, 0.02) * c.eff) + a_ns + split_ns;
+        return kLaunchNs + hbm_ns / (std::max(occ, 0.02) * c.cost.a) + a_ns + split_ns;
     }
     const double units = (double)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * pl.splits;
     const double slots = (double)kNumCUs * c.wgs_per_cu;
     const double rounds = std::ceil(units / slots);
-    const double ksplit = pl.sps * 128.0;
-    const double per_wg_ns = 2.0 * c.bm * c.bn * ksplit * c.wgs_per_cu / (kCuFlopPerNs * c.eff);
-    return std::max(rounds * per_wg_ns, hbm_ns) + split_ns;
+    const double per_cu = std::ceil(std::min(units, slots) / kNumCUs);
+    const double stage_us =
+        c.wgs_per_cu == 1 ? c.cost.a
+                          : c.cost.a + (c.cost.b - c.cost.a) * (per_cu - 1) / (c.wgs_per_cu - 1);
+    const int stages = c.persistent ? (pl.sps + 3) / 4 * 4 : pl.sps;
+    // Decode-sized M: a tiled kernel streams B only two stages ahead and
+    // leaves most MFMA rows empty; its HBM floor is taken at 60%.
+    const double floor_ns = M <= 32 ? hbm_ns / 0.6 : hbm_ns;
+    return kLaunchNs + std::max(rounds * (stages * stage_us + c.cost.c) * 1000.0, floor_ns) +
+           split_ns;
 }
 
 bool choose_plan(int M, int N, int K, size_t ws_avail, Plan* best)
@@ -1185,16 +1237,20 @@ bool choose_plan(int M, int N, int K, size_t ws_avail, Plan* best)
     bool have = false;
     double best_cost = 0;
     for (int i = 0; i < kNumConfigs; ++i) {
-        Plan pl;
-        if (!make_plan(i, 0, M, N, K, &pl)) continue;
-        if (pl.ws_bytes > ws_avail || pl.ws_bytes >= (1ull << 31)) {
-            if (!make_plan(i, 1, M, N, K, &pl)) continue;
-        }
-        const double cst = plan_cost(pl, M, N, K);
-        if (!have || cst < best_cost) {
-            *best = pl;
-            best_cost = cst;
-            have = true;
+        const bool skinny = kConfigs[i].family == kSkinny;
+        for (int want : {0, 1, 2, 4, 8}) {
+            if (skinny != (want == 0)) continue;  // skinny: its own split rule
+            Plan pl;
+            if (!make_plan(i, want, M, N, K, &pl)) continue;
+            if (pl.ws_bytes > ws_avail || pl.ws_bytes >= (1ull << 31)) {
+                if (!make_plan(i, 1, M, N, K, &pl)) continue;
+            }
+            const double cst = plan_cost(pl, M, N, K);
+            if (!have || cst < best_cost) {
+                *best = pl;
+                best_cost = cst;
+                have = true;
+            }
         }
     }
     return have;
