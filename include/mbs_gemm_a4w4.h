@@ -104,6 +104,18 @@ int mbs_quantize_mxfp4_bf16(const void* x, int rows, int K, uint8_t* packed,
                             uint8_t* scale_shuffled, uint8_t* scale_plain, int pad_byte,
                             void* stream);
 
+/* MBS quantization: as mbs_quantize_mxfp4_bf16, but each row is first
+ * scaled by its MBS multiplier 1 + f/256, where the factor byte f (written
+ * to factors[row]) is the top 8 mantissa bits of 6/max|row| (IEEE fp32
+ * division, truncated; a zero, infinite or NaN maximum gives 0).  Passing
+ * the factors of A and B to mbs_gemm_a4w4_launch undoes the multipliers
+ * (f(b) = 1/(1 + b/256)).  This is the factor computation the reference
+ * describes at docs/kernel_advanced.md:120-129 and consumes at
+ * kernel/gemm_a4w4.h:20-22; the reference ships no kernel for it. */
+int mbs_quantize_mxfp4_mbs_bf16(const void* x, int rows, int K, uint8_t* packed,
+                                uint8_t* scale_shuffled, uint8_t* scale_plain, uint8_t* factors,
+                                int pad_byte, void* stream);
+
 /* Plain packed weights [N, K/2] -> (16,16)-preshuffled [N, K/2] (out of place).
  * Replaces aiter.ops.shuffle.shuffle_weight(w, layout=(16,16))
  * (test_gemm_a4w4.py:141). */

@@ -73,6 +73,14 @@ def quantize_mxfp4(x, shuffle: bool = True, pad_byte: int = 127):
     return ext().quantize_mxfp4(x, shuffle, pad_byte)
 
 
+def quantize_mxfp4_mbs(x, shuffle: bool = True, pad_byte: int = 127):
+    """MBS quantization: bf16 [R,K] device tensor -> (packed, E8M0 scales,
+    factor bytes u8 [R]).  Row r is scaled by 1 + f[r]/256 (f = top 8
+    mantissa bits of 6/max|row r|) before quantization; passing the factors
+    of A and B to ``gemm_a4w4`` undoes the scaling in the epilogue."""
+    return ext().quantize_mxfp4_mbs(x, shuffle, pad_byte)
+
+
 def shuffle_weight(w):
     """(16,16) preshuffle of packed weights [N,K/2] (out of place)."""
     return ext().shuffle_weight(w)

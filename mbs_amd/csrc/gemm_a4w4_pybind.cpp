@@ -168,6 +168,31 @@ std::tuple<at::Tensor, at::Tensor> quantize_mxfp4(at::Tensor x, bool shuffle, in
     return {packed, scales};
 }
 
+// MBS quantization: (packed, scales, factor bytes [R]) -- rows scaled by
+// their MBS multipliers before quantization; pass the factors to gemm_a4w4.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> quantize_mxfp4_mbs(at::Tensor x, bool shuffle,
+                                                                  int64_t pad_byte)
+{
+    TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.scalar_type() == at::kBFloat16,
+                "quantize_mxfp4_mbs: x must be a 2D bf16 device tensor");
+    auto xc = x.contiguous();
+    const int64_t R = xc.size(0), K = xc.size(1);
+    TORCH_CHECK(K % 32 == 0, "quantize_mxfp4_mbs: K must be a multiple of 32");
+    c10::DeviceGuard guard(x.device());
+    auto opts = torch::TensorOptions().dtype(torch::kByte).device(x.device());
+    auto packed = torch::empty({R, K / 2}, opts);
+    at::Tensor scales = shuffle ? torch::empty({round_up(R, 32), scale_pad(K)}, opts)
+                                : torch::empty({R, K / 32}, opts);
+    auto factors = torch::empty({R}, opts);
+    check_status(mbs_quantize_mxfp4_mbs_bf16(
+                     xc.data_ptr(), (int)R, (int)K, packed.data_ptr<uint8_t>(),
+                     shuffle ? scales.data_ptr<uint8_t>() : nullptr,
+                     shuffle ? nullptr : scales.data_ptr<uint8_t>(), factors.data_ptr<uint8_t>(),
+                     (int)pad_byte, current_stream(x)),
+                 "quantize_mxfp4_mbs");
+    return {packed, scales, factors};
+}
+
 // Plain packed weights [N, K/2] -> (16,16)-preshuffled copy (shuffle_weight).
 at::Tensor shuffle_weight(at::Tensor w)
 {
@@ -238,6 +263,9 @@ PYBIND11_MODULE(mbs_gemm_a4w4, m)
           pybind11::arg("A_scale"), pybind11::arg("B_scale"),
           pybind11::arg("A_factor") = pybind11::none(), pybind11::arg("B_factor") = pybind11::none());
     m.def("quantize_mxfp4", &quantize_mxfp4, "bf16 -> (packed e2m1, E8M0 scales)",
+          pybind11::arg("x"), pybind11::arg("shuffle") = true, pybind11::arg("pad_byte") = 127);
+    m.def("quantize_mxfp4_mbs", &quantize_mxfp4_mbs,
+          "bf16 -> (packed e2m1, E8M0 scales, MBS factor bytes): rows scaled by 1 + f/256",
           pybind11::arg("x"), pybind11::arg("shuffle") = true, pybind11::arg("pad_byte") = 127);
     m.def("shuffle_weight", &shuffle_weight, "(16,16) preshuffle of packed weights",
           pybind11::arg("w"));

@@ -29,10 +29,77 @@ __device__ __forceinline__ int floor_log2_bits(uint32_t u)
     return (31 - __builtin_clz(u & 0x7FFFFFu)) - 149;
 }
 
-// One thread per 32-element K-block: amax -> E8M0, then e2m1 round to
-// nearest even on the code with saturation at 6.  The code of |q| is the
-// number of grid midpoints it passes: ties at 0.25, 1.25, 2.5, 5 go down to
-// the even code, ties at 0.75, 1.75, 3.5 go up to it.
+// Quantize one 32-element K-block (bf16 words w, two values each) scaled by
+// m: amax -> E8M0, then e2m1 round to nearest even on the code with
+// saturation at 6.  The code of |q| is the number of grid midpoints it
+// passes: ties at 0.25, 1.25, 2.5, 5 go down to the even code, ties at 0.75,
+// 1.75, 3.5 go up to it.  m is 1 or an MBS row multiplier 1 + b/256; every
+// product is exact in fp32 (8 + 9 significant bits) and positive scaling is
+// monotone, so the block maximum is the bf16 maximum times m.
+__device__ __forceinline__ void quantize_block(const uint32_t w[16], float m, uint32_t out[4],
+                                               uint32_t* scale)
+{
+    // bf16 -> fp32 bits is a 16-bit shift; track amax on the magnitude bits
+    // (monotone for non-NaN values) and NaN separately.
+    uint32_t amax_bits = 0;
+    bool nan = false;
+    for (int i = 0; i < 32; ++i) {
+        const uint32_t h = (i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xFFFF);
+        const uint32_t mg = (h & 0x7FFF) << 16;
+        nan |= mg > 0x7F800000u;
+        amax_bits = (mg > amax_bits && mg <= 0x7F800000u) ? mg : amax_bits;
+    }
+    const uint32_t amax_m = __float_as_uint(__uint_as_float(amax_bits) * m);
+    uint32_t s;
+    if (nan) s = 255;
+    else if (amax_m == 0) s = 0;
+    else if (amax_m >= 0x7F800000u) s = 254;
+    else {
+        int e = floor_log2_bits(amax_m) - 2 + 127;
+        s = (uint32_t)(e < 0 ? 0 : (e > 254 ? 254 : e));
+    }
+    // 2^(127 - s), s in [0, 254]: exponent field 254 - s, or the subnormal
+    // 2^-127 for s == 254.
+    const float inv = (s == 254) ? __uint_as_float(0x00400000u) : __uint_as_float((254u - s) << 23);
+    for (int i = 0; i < 4; ++i) out[i] = 0;
+    for (int i = 0; i < 32; ++i) {
+        const uint32_t h = (i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xFFFF);
+        const float q = (__uint_as_float((h & 0x7FFF) << 16) * m) * inv;
+        uint32_t c = (uint32_t)(q > 0.25f) + (uint32_t)(q >= 0.75f) + (uint32_t)(q > 1.25f) +
+                     (uint32_t)(q >= 1.75f) + (uint32_t)(q > 2.5f) + (uint32_t)(q >= 3.5f) +
+                     (uint32_t)(q > 5.0f);
+        c |= (h >> 12) & 8u;  // sign
+        if (nan) c = 0;
+        out[i >> 3] |= c << (4 * (i & 7));
+    }
+    *scale = s;
+}
+
+__device__ __forceinline__ void load_block(const uint16_t* p, uint32_t w[16])
+{
+    const i32x4* src = reinterpret_cast<const i32x4*>(p);
+    for (int i = 0; i < 4; ++i) {
+        const i32x4 v = src[i];
+        w[4 * i + 0] = v[0];
+        w[4 * i + 1] = v[1];
+        w[4 * i + 2] = v[2];
+        w[4 * i + 3] = v[3];
+    }
+}
+
+__device__ __forceinline__ void store_block(int r, int b, int K, int nb, int snp,
+                                            const uint32_t out[4], uint32_t s,
+                                            uint8_t* __restrict__ packed,
+                                            uint8_t* __restrict__ sshuf,
+                                            uint8_t* __restrict__ splain)
+{
+    i32x4 o = {(int)out[0], (int)out[1], (int)out[2], (int)out[3]};
+    *reinterpret_cast<i32x4*>(packed + (int64_t)r * (K >> 1) + b * 16) = o;
+    if (splain) splain[(int64_t)r * nb + b] = (uint8_t)s;
+    if (sshuf) sshuf[flat_s(r, b, snp)] = (uint8_t)s;
+}
+
+// One thread per 32-element K-block.
 __global__ void __launch_bounds__(256)
 quantize_bf16_kernel(const uint16_t* __restrict__ x, int rows, int K, uint8_t* __restrict__ packed,
                      uint8_t* __restrict__ sshuf, uint8_t* __restrict__ splain, int snp)
@@ -41,51 +108,57 @@ quantize_bf16_kernel(const uint16_t* __restrict__ x, int rows, int K, uint8_t* _
     const int64_t blk = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (blk >= (int64_t)rows * nb) return;
     const int r = (int)(blk / nb), b = (int)(blk - (int64_t)r * nb);
-    const i32x4* src = reinterpret_cast<const i32x4*>(x + (int64_t)r * K + b * 32);
-    uint32_t w[16];
-    for (int i = 0; i < 4; ++i) {
-        const i32x4 v = src[i];
-        w[4 * i + 0] = v[0];
-        w[4 * i + 1] = v[1];
-        w[4 * i + 2] = v[2];
-        w[4 * i + 3] = v[3];
+    uint32_t w[16], out[4], s;
+    load_block(x + (int64_t)r * K + b * 32, w);
+    quantize_block(w, 1.0f, out, &s);
+    store_block(r, b, K, nb, snp, out, s, packed, sshuf, splain);
+}
+
+// MBS quantization (docs/kernel_advanced.md:120-129 of the reference): one
+// workgroup per row.  The row's absolute maximum gives the factor byte b =
+// the top 8 mantissa bits of 6/max (IEEE division, then truncation; a zero,
+// infinite or NaN maximum gives 0); the row is then quantized block by block
+// after scaling by 1 + b/256, which the GEMM's factor epilogue
+// f(b) = 1/(1 + b/256) undoes.
+__global__ void __launch_bounds__(256)
+quantize_mbs_bf16_kernel(const uint16_t* __restrict__ x, int K, uint8_t* __restrict__ packed,
+                         uint8_t* __restrict__ sshuf, uint8_t* __restrict__ splain,
+                         uint8_t* __restrict__ factors, int snp)
+{
+    __shared__ uint32_t red[4];
+    const int r = blockIdx.x;
+    const uint16_t* xr = x + (int64_t)r * K;
+    // row maximum on the magnitude bits; a NaN maps above every number
+    uint32_t amax = 0;
+    for (int e = threadIdx.x * 8; e < K; e += 256 * 8) {
+        const i32x4 v = *reinterpret_cast<const i32x4*>(xr + e);
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t h = ((uint32_t)v[i >> 1] >> (16 * (i & 1))) & 0x7FFF;
+            amax = h > amax ? h : amax;
+        }
     }
-    // bf16 -> fp32 bits is a 16-bit shift; track amax on the magnitude bits
-    // (monotone for non-NaN values) and NaN separately.
-    uint32_t amax_bits = 0;
-    bool nan = false;
-    for (int i = 0; i < 32; ++i) {
-        const uint32_t h = (i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xFFFF);
-        const uint32_t m = (h & 0x7FFF) << 16;
-        nan |= m > 0x7F800000u;
-        amax_bits = (m > amax_bits && m <= 0x7F800000u) ? m : amax_bits;
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)amax, off);
+        amax = o > amax ? o : amax;
     }
-    uint32_t s;
-    if (nan) s = 255;
-    else if (amax_bits == 0) s = 0;
-    else if (amax_bits == 0x7F800000u) s = 254;
-    else {
-        int e = floor_log2_bits(amax_bits) - 2 + 127;
-        s = (uint32_t)(e < 0 ? 0 : (e > 254 ? 254 : e));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = red[0];
+    for (int i = 1; i < 4; ++i) amax = red[i] > amax ? red[i] : amax;
+    uint32_t fb = 0;
+    if (amax != 0 && amax < 0x7F80) {  // finite, non-zero
+        const float q = __fdiv_rn(6.0f, __uint_as_float(amax << 16));
+        fb = (__float_as_uint(q) >> 15) & 0xFF;
     }
-    // 2^(127 - s), s in [0, 254]: exponent field 254 - s, or the subnormal
-    // 2^-127 for s == 254.
-    const float inv = (s == 254) ? __uint_as_float(0x00400000u) : __uint_as_float((254u - s) << 23);
-    uint32_t out[4] = {0, 0, 0, 0};
-    for (int i = 0; i < 32; ++i) {
-        const uint32_t h = (i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xFFFF);
-        const float q = __uint_as_float((h & 0x7FFF) << 16) * inv;
-        uint32_t c = (uint32_t)(q > 0.25f) + (uint32_t)(q >= 0.75f) + (uint32_t)(q > 1.25f) +
-                     (uint32_t)(q >= 1.75f) + (uint32_t)(q > 2.5f) + (uint32_t)(q >= 3.5f) +
-                     (uint32_t)(q > 5.0f);
-        c |= (h >> 12) & 8u;  // sign
-        if (nan) c = 0;
-        out[i >> 3] |= c << (4 * (i & 7));
+    const float m = __uint_as_float(0x3F800000u | (fb << 15));
+    if (threadIdx.x == 0) factors[r] = (uint8_t)fb;
+    const int nb = K >> 5;
+    for (int b = threadIdx.x; b < nb; b += 256) {
+        uint32_t w[16], out[4], s;
+        load_block(xr + b * 32, w);
+        quantize_block(w, m, out, &s);
+        store_block(r, b, K, nb, snp, out, s, packed, sshuf, splain);
     }
-    i32x4 o = {(int)out[0], (int)out[1], (int)out[2], (int)out[3]};
-    *reinterpret_cast<i32x4*>(packed + (int64_t)r * (K >> 1) + b * 16) = o;
-    if (splain) splain[(int64_t)r * nb + b] = (uint8_t)s;
-    if (sshuf) sshuf[flat_s(r, b, snp)] = (uint8_t)s;
 }
 
 // Padding entries of a shuffled scale buffer (rows >= R or blocks >= nb).
@@ -207,6 +280,29 @@ int mbs_quantize_mxfp4_bf16(const void* x, int rows, int K, uint8_t* packed,
     hipLaunchKernelGGL(quantize_bf16_kernel, dim3(blocks_for((int64_t)rows * nb)), dim3(256), 0,
                        s, static_cast<const uint16_t*>(x), rows, K, packed, scale_shuffled,
                        scale_plain, snp);
+    return launched();
+}
+
+int mbs_quantize_mxfp4_mbs_bf16(const void* x, int rows, int K, uint8_t* packed,
+                                uint8_t* scale_shuffled, uint8_t* scale_plain, uint8_t* factors,
+                                int pad_byte, void* stream)
+{
+    if (!x || !packed || !factors) return fmt_fail("null pointer");
+    if (rows < 1 || K < 32 || K % 32) return fmt_fail("need rows >= 1 and K % 32 == 0");
+    if (pad_byte < 0 || pad_byte > 255) return fmt_fail("pad_byte must be a byte");
+    (void)hipGetLastError();
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int snp = scale_pad_of(K);
+    const int nb = K / 32;
+    if (scale_shuffled) {
+        const int64_t n = (int64_t)((rows + 31) & ~31) * snp;
+        if ((rows % 32) || nb != snp)
+            hipLaunchKernelGGL(scale_pad_kernel, dim3(blocks_for(n)), dim3(256), 0, s,
+                               scale_shuffled, rows, nb, snp, (uint8_t)pad_byte);
+    }
+    hipLaunchKernelGGL(quantize_mbs_bf16_kernel, dim3(rows), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(x), K, packed, scale_shuffled, scale_plain,
+                       factors, snp);
     return launched();
 }
 

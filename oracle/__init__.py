@@ -66,6 +66,10 @@ def lib() -> ctypes.CDLL:
         L.oracle_flat_s.argtypes = [I, I, I]
         L.oracle_flat_s.restype = I
         L.oracle_quantize_mxfp4.argtypes = [P, I, I, P, P]
+        L.oracle_quantize_mxfp4_mbs.argtypes = [P, I, I, P, P, P]
+        L.oracle_quantize_mxfp4_mbs.restype = None
+        L.oracle_mbs_factor_byte.argtypes = [ctypes.c_float]
+        L.oracle_mbs_factor_byte.restype = ctypes.c_uint8
         L.oracle_dequant_mxfp4.argtypes = [P, P, I, I, P]
         L.oracle_shuffle_b.argtypes = [P, I, I, P]
         L.oracle_unshuffle_b.argtypes = [P, I, I, P]
@@ -136,6 +140,26 @@ def quantize_mxfp4(x) -> tuple[np.ndarray, np.ndarray]:
     scales = np.empty((R, K // 32), dtype=np.uint8)
     lib().oracle_quantize_mxfp4(_ptr(x), R, K, _ptr(packed), _ptr(scales))
     return packed, scales
+
+
+def mbs_factor_byte(amax: float) -> int:
+    """MBS factor byte of a row maximum: top 8 mantissa bits of 6/amax."""
+    return int(lib().oracle_mbs_factor_byte(float(amax)))
+
+
+def quantize_mxfp4_mbs(x) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """MBS quantization (docs/kernel_advanced.md:120-129 of the reference):
+    fp32/bf16-valued [R, K] -> (packed u8 [R, K/2], plain E8M0 u8 [R, K/32],
+    factor bytes u8 [R]); row r is quantized after scaling by 1 + f[r]/256."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    R, K = x.shape
+    if K % 32:
+        raise ValueError("K must be a multiple of 32")
+    packed = np.empty((R, K // 2), dtype=np.uint8)
+    scales = np.empty((R, K // 32), dtype=np.uint8)
+    factors = np.empty((R,), dtype=np.uint8)
+    lib().oracle_quantize_mxfp4_mbs(_ptr(x), R, K, _ptr(packed), _ptr(scales), _ptr(factors))
+    return packed, scales, factors
 
 
 def dequant_mxfp4(packed, scales) -> np.ndarray:

@@ -27,6 +27,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* ------------------------------------------------------------------ bits */
@@ -144,6 +145,51 @@ void oracle_quantize_mxfp4(const float* x, int64_t rows, int64_t K,
                 out[i] = (uint8_t)(codes[2 * i] | (codes[2 * i + 1] << 4));
         }
     }
+}
+
+/* --------------------------------------------------- MBS row factors ---- */
+
+/* MBS factor byte of a row with absolute maximum amax, after
+ * docs/kernel_advanced.md:120-125 of the reference: scale = 6.0 / max, and
+ * the factor is the top 8 bits of scale's fp32 mantissa (fp32 division,
+ * round to nearest even, then truncation).  A zero, infinite or NaN maximum
+ * gives 0 (factor 1.0): 6/0 and 6/tiny overflow to +inf, whose mantissa is 0. */
+uint8_t oracle_mbs_factor_byte(float amax)
+{
+    if (!(amax > 0.0f) || amax == INFINITY) return 0;
+    volatile float s = 6.0f / amax;  /* IEEE single division */
+    return (uint8_t)((f32_bits(s) >> 15) & 0xFF);
+}
+
+/* MBS quantization of rows: factor byte b per row from its absolute
+ * maximum, the row multiplied by 1 + b/256 (the bits 0x3F800000 | b << 15:
+ * the "1.xxxxx" of docs/kernel_advanced.md:128), then ordinary MXFP4
+ * quantization.  The GEMM epilogue's f(b) = 1/(1 + b/256)
+ * (test_gemm_a4w4.py:47-51) undoes the multiplier.  For bf16-valued inputs
+ * the product is exact in fp32 (8 + 9 significant bits).  A row holding a
+ * NaN gets factor 0. */
+void oracle_quantize_mxfp4_mbs(const float* x, int64_t rows, int64_t K,
+                               uint8_t* packed, uint8_t* scales, uint8_t* factors)
+{
+    float* row = (float*)malloc((size_t)K * sizeof(float));
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * K;
+        float amax = 0.0f;
+        int nan = 0;
+        for (int64_t k = 0; k < K; ++k) {
+            float a = fabsf(xr[k]);
+            if (a != a) nan = 1;
+            else if (a > amax) amax = a;
+        }
+        const uint8_t b = nan ? 0 : oracle_mbs_factor_byte(amax);
+        const uint32_t mb = 0x3F800000u | ((uint32_t)b << 15);
+        float m;
+        memcpy(&m, &mb, 4);
+        for (int64_t k = 0; k < K; ++k) row[k] = xr[k] * m;
+        factors[r] = b;
+        oracle_quantize_mxfp4(row, 1, K, packed + r * (K / 2), scales + r * (K / 32));
+    }
+    free(row);
 }
 
 /* ------------------------------------------------------------ dequantize */
