@@ -30,7 +30,13 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["gemm_a4w4.hip", "mxfp4_format.hip"]
+# The GEMM kernel families are instantiated in separate translation units
+# (gemm_inst_*.hip) so that they compile in parallel.
+HIP_SOURCES = [
+    "gemm_inst_bdirect_c.hip", "gemm_inst_bdirect_d.hip", "gemm_inst_bdirect_a.hip",
+    "gemm_inst_bdirect_b.hip", "gemm_inst_tiled.hip", "gemm_inst_skinny.hip",
+    "gemm_a4w4.hip", "mxfp4_format.hip",
+]
 HIP_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     # packed-fp32 VALU ops are kept out of the generated code on purpose
@@ -59,7 +65,8 @@ def _hip_object(src: str) -> str:
 
 def build_kernel_lib() -> str:
     os.makedirs(LIB, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=len(HIP_SOURCES)) as ex:
+    workers = max(1, min(len(HIP_SOURCES), os.cpu_count() or 1, 16))
+    with cf.ThreadPoolExecutor(max_workers=workers) as ex:
         objs = list(ex.map(_hip_object, HIP_SOURCES))
     tmp = KERNEL_LIB + ".tmp"
     _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp])

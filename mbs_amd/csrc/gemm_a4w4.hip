@@ -22,8 +22,7 @@
 //    of a workgroup split K and reduce through LDS in a fixed order.
 //  * splitk_reduce_kernel -- deterministic fixed-order sum of fp32 split-K
 //    partials plus the same epilogue.
-#include "mxfp4_device.h"
-#include "mbs_gemm_a4w4.h"
+#include "gemm_kernels.h"
 
 #include <algorithm>
 #include <cstdio>
@@ -37,942 +36,12 @@ thread_local std::string g_last_error;
 }
 void set_last_error(const char* msg) { g_last_error = msg ? msg : ""; }
 
-__constant__ FactorTable kFactors = FactorTable();
-
-__device__ __forceinline__ float factor_of(uint32_t b)
-{
-    return __uint_as_float(kFactors.bits[b & 255]);
-}
-
-struct GemmArgs {
-    const uint8_t* A;
-    const uint8_t* B;
-    const uint8_t* As;
-    const uint8_t* Bs;
-    const uint8_t* Af;  // nullable (both or neither)
-    const uint8_t* Bf;
-    uint16_t* out;      // bf16 [Mpad, N]
-    float* ws;          // split-K partials [splits][M][N] fp32, or null
-    int M, N, K, snp;   // snp = scaleN_pad
-    int tiles_m, tiles_n;
-    int splits, sps;    // K-splits and 128-K stages per split (even)
-};
-
-// ======================================================================
-// Tiled kernel
-// ======================================================================
-template <int BM_, int BN_, int WGM_, int WGN_>
-struct TileShape {
-    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
-    static constexpr int NW = WGM * WGN, NT = 64 * NW;
-    static constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile
-    static constexpr int FM = WM / 16, FN = WN / 16;    // 16x16 fragments per wave
-    static constexpr int AF = BM / 16, BF = BN / 16;    // 1-KiB fragments per stage
-    static constexpr int DA = AF / NW, DB = BF / NW;    // data DMAs per wave per stage
-    static constexpr int SGA = BM / 32, SGB = BN / 32;  // 256-B scale groups per 256 K
-    static constexpr int DS = (SGA + SGB + NW - 1) / NW;  // scale DMAs per wave per group
-    static constexpr int SA = FM / 2, SB = FN / 2;      // scale dwords per wave per group
-    static constexpr int STAGE = (AF + BF) * 1024;
-    static constexpr int SCB = DS * NW * 256;
-    static constexpr int NBUF = 4, PF = 3;
-    static_assert(AF % NW == 0 && BF % NW == 0, "fragments must split evenly over waves");
-    static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
-    static_assert(NBUF * STAGE + 2 * SCB <= 160 * 1024, "LDS budget");
-};
-
-template <class T, bool KTAIL, bool SPLIT>
-__global__ void __launch_bounds__(T::NT) gemm_tiled_kernel(const GemmArgs p)
-{
-    // One __shared__ object per ring slot: the compiler tracks in-flight LDS
-    // DMA per LDS object (alias scopes), so distinct objects let it see that
-    // reading slot s does not wait on the DMA into slot s+1..s+3.
-    __shared__ __attribute__((aligned(1024))) uint8_t sd0[T::STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t sd1[T::STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t sd2[T::STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t sd3[T::STAGE];
-    __shared__ __attribute__((aligned(256))) uint8_t ss0[T::SCB];
-    __shared__ __attribute__((aligned(256))) uint8_t ss1[T::SCB];
-    auto sdata = [&](auto B) __attribute__((always_inline)) -> uint8_t* {
-        constexpr int b = decltype(B)::value;
-        if constexpr (b == 0) return sd0;
-        else if constexpr (b == 1) return sd1;
-        else if constexpr (b == 2) return sd2;
-        else return sd3;
-    };
-    auto sscale = [&](auto S) __attribute__((always_inline)) -> uint8_t* {
-        if constexpr (decltype(S)::value == 0) return ss0;
-        else return ss1;
-    };
-
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = w / T::WGN, wn = w % T::WGN;
-
-    // ---- tile / split assignment: XCD-aware, grouped along M -----------
-    // Workgroups are dealt round-robin over the 8 XCDs; renumber so that
-    // consecutive logical ids share an XCD (and its L2), then walk tiles in
-    // groups of 8 tile-rows so concurrently running tiles share A and B.
-    int bid = blockIdx.x;
-    const int G = gridDim.x;
-    if ((G & 7) == 0) bid = (bid & 7) * (G >> 3) + (bid >> 3);
-    const int tiles = p.tiles_m * p.tiles_n;
-    const int split = bid / tiles;
-    const int t = bid - split * tiles;
-    constexpr int GROUP = 8;
-    const int grp = t / (GROUP * p.tiles_n);
-    const int first_m = grp * GROUP;
-    const int gsz = min(p.tiles_m - first_m, GROUP);
-    const int tin = t - grp * GROUP * p.tiles_n;
-    const int m0 = (first_m + tin % gsz) * T::BM;
-    const int n0 = (tin / gsz) * T::BN;
-
-    const int K = p.K, Kp = K >> 1;
-    const int S_total = (K + 127) >> 7;
-    const int s_begin = split * p.sps;
-    const int n_st = min(p.sps, S_total - s_begin);
-
-    // ---- buffer resources (tile-based so offsets stay small) -----------
-    const int rows_a = min(T::BM, p.M - m0);
-    const int rows_b = min(T::BN, p.N - n0);
-    const int Mpad = (p.M + 31) & ~31, Npad = (p.N + 31) & ~31;
-    const rsrc_t rA = make_rsrc(p.A + (size_t)m0 * Kp, (uint32_t)(rows_a * Kp));
-    const rsrc_t rB = make_rsrc(p.B + (size_t)(n0 >> 4) * K * 8, (uint32_t)(rows_b * Kp));
-    const rsrc_t rAs = make_rsrc(p.As + (size_t)(m0 >> 5) * 32 * p.snp,
-                                 (uint32_t)(min(T::BM, Mpad - m0) * p.snp));
-    const rsrc_t rBs = make_rsrc(p.Bs + (size_t)(n0 >> 5) * 32 * p.snp,
-                                 (uint32_t)(min(T::BN, Npad - n0) * p.snp));
-
-    // ---- per-lane DMA offsets ------------------------------------------
-    // A fragment f, lane i: row 16f + i%16, K-block i/16 of the stage.
-    // B fragment f, lane i: preshuffled, 16 contiguous bytes at i*16.
-    uint32_t voA[T::DA], voB[T::DB];
-    static_for<T::DA>([&](auto d) {
-        const int fa = w * T::DA + d;
-        voA[d] = (uint32_t)((16 * fa + (lane & 15)) * Kp + (lane >> 4) * 16);
-    });
-    static_for<T::DB>([&](auto d) {
-        const int fb = w * T::DB + d;
-        voB[d] = (uint32_t)(fb * K * 8 + lane * 16);
-    });
-    const bool hi_lane = lane >= 32;  // K-blocks 2,3 of a 128-K stage
-    const uint32_t hi_bit = hi_lane ? kOOB : 0u;
-
-    // ---- DMA items ---------------------------------------------------------
-    // One stage's DMA group: DA fragments of A, DB of B and, on the first
-    // stage of a 256-K group, DS scale groups.  Stages past the split's end
-    // are still issued, with every lane out of range: they write zeros into a
-    // free slot and keep the per-stage VMEM count uniform, which the vmcnt
-    // bookkeeping relies on.  The out-of-range bit is OR-ed in rather than
-    // selected: a select on a wave-uniform condition gets turned into a
-    // branch that would split the pipelined loop body.
-    auto dead_bits = [&](int ls) __attribute__((always_inline)) {
-        const int s = s_begin + ls;
-        uint32_t dead = (uint32_t)(ls >= n_st) << 31;
-        if (KTAIL) dead |= ((uint32_t)(s == S_total - 1) << 31) & hi_bit;
-        asm volatile("" : "+v"(dead));
-        return dead;
-    };
-    auto issue_item = [&](auto BUF, auto D, int ls, uint32_t dead) __attribute__((always_inline)) {
-        constexpr int d = decltype(D)::value;
-        const int s = s_begin + ls;
-        if constexpr (d < T::DA) {
-            dma16(rA, sdata(BUF) + (w * T::DA + d) * 1024, (voA[d] + (uint32_t)s * 64u) | dead);
-        } else if constexpr (d < T::DA + T::DB) {
-            constexpr int e = d - T::DA;
-            dma16(rB, sdata(BUF) + (T::AF + w * T::DB + e) * 1024,
-                  (voB[e] + (uint32_t)s * 1024u) | dead);
-        } else {
-            constexpr int e = d - T::DA - T::DB;
-            constexpr int slot = (decltype(BUF)::value >> 1) & 1;
-            const int q = w * T::DS + e;
-            const bool is_a = q < T::SGA;
-            const bool is_b = !is_a && q < T::SGA + T::SGB;
-            const uint32_t g = (uint32_t)(s >> 1) * 256u + lane * 4;
-            const uint32_t qdead = ((uint32_t)(ls >= n_st) | (uint32_t)!(is_a || is_b)) << 31;
-            const uint32_t base = (uint32_t)((is_a ? q : q - T::SGA) * 32 * p.snp);
-            dma4(is_a ? rAs : rBs, sscale(std::integral_constant<int, slot>{}) + q * 256,
-                 (base + g) | qdead);
-        }
-    };
-    // VMEM ops one wave issues per local stage (static parity).
-    constexpr int CNT_ODD = T::DA + T::DB;
-    constexpr int CNT_EVEN = T::DA + T::DB + T::DS;
-
-    i32x4 ra[2][T::FM], rb[2][T::FN];
-    int sa[2][T::SA], sb[2][T::SB];
-    f32x4 acc[T::FM][T::FN];
-    static_for<T::FM>([&](auto i) {
-        static_for<T::FN>([&](auto j) { acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f}; });
-    });
-
-    // ---- LDS read items: stage in slot BUF -> register set R ----------------
-    auto read_item = [&](auto BUF, auto R, auto X) __attribute__((always_inline)) {
-        constexpr int r = decltype(R)::value;
-        constexpr int x = decltype(X)::value;
-        constexpr int slot = (decltype(BUF)::value >> 1) & 1;
-        if constexpr (x < T::FM) {
-            ra[r][x] = *reinterpret_cast<const i32x4*>(sdata(BUF) + (wm * T::FM + x) * 1024 +
-                                                       lane * 16);
-        } else if constexpr (x < T::FM + T::FN) {
-            constexpr int j = x - T::FM;
-            rb[r][j] = *reinterpret_cast<const i32x4*>(
-                sdata(BUF) + (T::AF + wn * T::FN + j) * 1024 + lane * 16);
-        } else if constexpr (x < T::FM + T::FN + T::SA) {
-            constexpr int i = x - T::FM - T::FN;
-            sa[slot][i] = *reinterpret_cast<const int*>(
-                sscale(std::integral_constant<int, slot>{}) + ((wm * T::WM) / 32 + i) * 256 +
-                lane * 4);
-        } else {
-            constexpr int j = x - T::FM - T::FN - T::SA;
-            sb[slot][j] = *reinterpret_cast<const int*>(
-                sscale(std::integral_constant<int, slot>{}) +
-                (T::SGA + (wn * T::WN) / 32 + j) * 256 + lane * 4);
-        }
-    };
-    auto read_all = [&](auto BUF, auto R) __attribute__((always_inline)) {
-        constexpr int NX = T::FM + T::FN + (((decltype(BUF)::value & 1) == 0) ? T::SA + T::SB : 0);
-        static_for<NX>([&](auto X) { read_item(BUF, R, X); });
-    };
-
-    // ---- one pipelined stage ----------------------------------------------
-    // Compute stage ls (slot u, registers u&1) while issuing the DMA group of
-    // stage ls+3 and the LDS reads of stage ls+1.  The work is cut into FM
-    // chunks (one A-fragment row of FN MFMAs each) and each chunk carries an
-    // even share of the DMAs and LDS reads; sched_barrier(0) between chunks
-    // keeps the compiler from clustering the reads behind the MFMAs.
-    auto stage = [&](auto U, int ls) __attribute__((always_inline)) {
-        constexpr int u = decltype(U)::value;
-        constexpr int r = u & 1, slot = (u >> 1) & 1, h = u & 1;
-        using BUFN = std::integral_constant<int, (u + 1) & 3>;  // slot read now
-        using BUFD = std::integral_constant<int, (u + 3) & 3>;  // slot refilled now
-        using RN = std::integral_constant<int, (u + 1) & 1>;
-        constexpr int NDMA = T::DA + T::DB + ((((u + 3) & 1) == 0) ? T::DS : 0);
-        constexpr int NRD = T::FM + T::FN + ((((u + 1) & 1) == 0) ? T::SA + T::SB : 0);
-        constexpr int NCH = T::FM;
-
-        // stage ls+1 must have landed for every wave; ls+2 may be in flight
-        wait_vmcnt<((u & 1) == 0) ? CNT_EVEN : CNT_ODD>();
-        barrier();
-        __builtin_amdgcn_sched_barrier(0);
-
-        const uint32_t dead = dead_bits(ls + 3);
-        int sav[T::SA], sbv[T::SB];
-        static_for<T::SA>([&](auto i) { sav[i] = sa[slot][i]; });
-        static_for<T::SB>([&](auto j) { sbv[j] = sb[slot][j]; });
-        if constexpr (KTAIL) {
-            // Blocks past K (zeroed data) get a finite scale so 0 * scale
-            // cannot become NaN when the caller's padding bytes are 0xFF.
-            const bool tail = (s_begin + ls == S_total - 1) && hi_lane;
-            static_for<T::SA>([&](auto i) { sav[i] = tail ? 0x7F7F7F7F : sav[i]; });
-            static_for<T::SB>([&](auto j) { sbv[j] = tail ? 0x7F7F7F7F : sbv[j]; });
-        }
-        static_for<NCH>([&](auto C) {
-            constexpr int c = decltype(C)::value;
-            static_for<NDMA>([&](auto D) {
-                if constexpr (D * NCH / NDMA == c) issue_item(BUFD{}, D, ls + 3, dead);
-            });
-            static_for<NRD>([&](auto X) {
-                if constexpr (X * NCH / NRD == c) read_item(BUFN{}, RN{}, X);
-            });
-            static_for<T::FN>([&](auto j) {
-                constexpr int opb = (j & 1) + 2 * h;
-                constexpr int opa = (c & 1) + 2 * h;
-                mfma_fp4<opb, opa>(acc[c][j], rb[r][j], ra[r][c], sbv[j / 2], sav[c / 2]);
-            });
-            __builtin_amdgcn_sched_barrier(0);
-        });
-    };
-
-    // ---- prologue --------------------------------------------------------
-    static_for<3>([&](auto P) {
-        constexpr int ps = decltype(P)::value;
-        constexpr int nd = T::DA + T::DB + (((ps & 1) == 0) ? T::DS : 0);
-        const uint32_t dead = dead_bits(ps);
-        static_for<nd>([&](auto D) { issue_item(P, D, ps, dead); });
-    });
-    wait_vmcnt<CNT_ODD + CNT_EVEN>();
-    barrier();
-    read_all(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
-
-    // ---- main loop: 4 stages per trip, ring slot = stage % 4 ----------
-    // The stage count is padded to a multiple of 4 with all-zero stages
-    // (zero data, zero scale bytes), which add exactly 0 to the sums.
-    const int n_st4 = (n_st + 3) & ~3;
-    for (int ls0 = 0; ls0 < n_st4; ls0 += 4) {
-        static_for<4>([&](auto U) { stage(U, ls0 + decltype(U)::value); });
-    }
-    // The look-ahead DMAs of the last trip are still writing LDS: drain them
-    // before this workgroup's LDS can be handed to another.
-    wait_vmcnt<0>();
-    mfma_drain();
-
-    // ---- epilogue ----------------------------------------------------------
-    // Factors default to 1.0f, and x * (1.0f * 1.0f) == x exactly, so the
-    // no-factor case runs the same branch-free code.
-    const bool has_f = (p.Af != nullptr) && (p.Bf != nullptr);
-    const int row_l = wm * T::WM + (lane & 15);        // row within tile (frag 0)
-    const int col_w = n0 + wn * T::WN;                  // first column of the wave
-    const int colq = (lane >> 4) * 4;                   // lane's 4 columns in a frag
-    if constexpr (SPLIT) {
-        const rsrc_t rW = make_rsrc(p.ws + ((size_t)split * p.M + m0) * p.N,
-                                    (uint32_t)(rows_a * p.N * 4));
-        static_for<T::FN>([&](auto j) {
-            const int c = col_w + j * 16;
-            if (c < p.N) {
-                static_for<T::FM>([&](auto i) {
-                    store16(rW, (uint32_t)(((row_l + i * 16) * p.N + c + colq) * 4), acc[i][j]);
-                });
-            }
-        });
-    } else {
-        const rsrc_t rAf = make_rsrc(p.Af + m0, has_f ? (uint32_t)rows_a : 0u);
-        const rsrc_t rBf = make_rsrc(p.Bf, has_f ? (uint32_t)p.N : 0u);
-        const rsrc_t rO = make_rsrc(p.out + (size_t)m0 * p.N, (uint32_t)(rows_a * p.N * 2));
-        float fa[T::FM];
-        static_for<T::FM>([&](auto i) {
-            fa[i] = has_f ? factor_of(load1(rAf, row_l + i * 16)) : 1.0f;
-        });
-        static_for<T::FN>([&](auto j) {
-            const int c = col_w + j * 16;
-            if (c < p.N) {
-                const uint32_t bytes = (uint32_t)load4(rBf, c + colq);
-                float fb[4];
-                for (int q = 0; q < 4; ++q) fb[q] = has_f ? factor_of(bytes >> (8 * q)) : 1.0f;
-                static_for<T::FM>([&](auto i) {
-                    f32x4 v = acc[i][j];
-                    for (int q = 0; q < 4; ++q) v[q] = v[q] * (fa[i] * fb[q]);
-                    store8(rO, (uint32_t)(((row_l + i * 16) * p.N + c + colq) * 2),
-                           pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-                });
-            }
-        });
-    }
-}
-
-// ======================================================================
-// B-direct tiled kernel
-// ======================================================================
-// Same workgroup tiling as gemm_tiled_kernel, but only A goes through LDS:
-// the preshuffled B is already in MFMA fragment order (one 1-KiB
-// contiguous block per 16 rows x 128 K), so each wave loads its B fragments
-// with plain 16-byte buffer loads straight into VGPRs, three stages ahead,
-// into a 4-deep register ring.  Scale dwords (one per lane per 32-row group
-// and 256-K group) are likewise loaded straight into VGPRs.  This halves the
-// LDS traffic of the stage (LDS bandwidth, not the MFMA pipe, is what limits
-// the all-LDS design), and A fragments are read from LDS just in time, two
-// MFMA rows ahead.  The epilogue turns each pair of 16-column fragments into
-// 16-byte row segments with two rounds of permlane swaps before storing.
-template <int BM_, int BN_, int WGM_, int WGN_>
-struct BdShape {
-    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
-    static constexpr int NW = WGM * WGN, NT = 64 * NW;
-    static constexpr int WM = BM / WGM, WN = BN / WGN;
-    static constexpr int FM = WM / 16, FN = WN / 16;
-    static constexpr int AF = BM / 16;                  // A fragments per stage
-    static constexpr int DA = (AF + NW - 1) / NW;       // A DMAs per wave per stage
-    static constexpr int SA = FM / 2, SB = FN / 2;      // scale dwords per wave per group
-    static constexpr int ASLOT = AF * 1024;             // bytes of one A ring slot
-    // Scales of a 256-K group: one 256-byte chunk per 32 rows (A) or columns
-    // (B), gathered four chunks per 16-byte LDS DMA.
-    static constexpr int CA = BM / 32, CB = BN / 32;
-    static constexpr int NSDA = (CA + 3) / 4, NSDB = (CB + 3) / 4, NSD = NSDA + NSDB;
-    static constexpr int NSDW = (NSD + NW - 1) / NW;    // scale DMAs per wave per group
-    static constexpr int SBUF = NSD * 1024;             // bytes of one scale buffer
-    static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
-    // MBS factor bytes of a unit in LDS: A rows at [0, 256), B columns in
-    // NBC chunks of 256 after them.
-    static constexpr int NBC = (BN + 255) / 256;
-    static constexpr int FBW = 256 * (1 + NBC);
-    static_assert(BM <= 256, "one 256-byte chunk of A factor bytes");
-    static_assert(NW == 1 ? NBC == 1 : NW >= 1 + NBC, "one factor DMA per wave");
-    static_assert(4 * ASLOT + 2 * SBUF <= 150 * 1024, "LDS budget");
-};
-
-// One work unit of the persistent schedule (a tile and a K-split of it);
-// every field is wave-uniform.
-struct Unit {
-    int m0, n0;    // tile origin
-    int split;     // K-split index
-    int sbeg, nst; // first 128-K stage and number of stages of the split
-    int valid;     // 0: past the end of this workgroup's unit list
-};
-
-// Persistent B-direct kernel: gridDim.x workgroups (at most one resident
-// set per CU) walk work units id = blockIdx.x + i*gridDim.x.  Per unit the
-// K loop runs n_st4 = round_up(sps, 4) stages (stages past the split end are
-// dead: their loads read zeros).  The software pipeline crosses unit
-// boundaries: the last four stages of a unit already prefetch the next
-// unit's first three stages and scale group, so the next unit's MFMAs start
-// right after this unit's epilogue, and no workgroup relaunch (with its
-// pipeline fill and store drain) happens between tiles.
-template <class T, bool KTAIL, bool SPLIT>
-__global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
-{
-    __shared__ __attribute__((aligned(1024))) uint8_t sa0[T::ASLOT];
-    __shared__ __attribute__((aligned(1024))) uint8_t sa1[T::ASLOT];
-    __shared__ __attribute__((aligned(1024))) uint8_t sa2[T::ASLOT];
-    __shared__ __attribute__((aligned(1024))) uint8_t sa3[T::ASLOT];
-    // MBS factor bytes of a unit (A rows at [0,256), B columns at [256,512)),
-    // double-buffered by unit parity, and the byte -> fp32 factor table.
-    __shared__ __attribute__((aligned(16))) uint8_t fbytes[2][T::FBW];
-    __shared__ __attribute__((aligned(16))) uint8_t fjunk[1024];  // target of filler DMAs
-    // Scale groups, double-buffered by group parity.
-    __shared__ __attribute__((aligned(1024))) uint8_t sc0[T::SBUF];
-    __shared__ __attribute__((aligned(1024))) uint8_t sc1[T::SBUF];
-    __shared__ float ftab[256];
-    auto aslot = [&](auto B) __attribute__((always_inline)) -> uint8_t* {
-        constexpr int b = decltype(B)::value & 3;
-        if constexpr (b == 0) return sa0;
-        else if constexpr (b == 1) return sa1;
-        else if constexpr (b == 2) return sa2;
-        else return sa3;
-    };
-
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = w / T::WGN, wn = w % T::WGN;
-
-    const int K = p.K, Kp = K >> 1;
-    const int S_total = (K + 127) >> 7;
-    const int n_st4 = (p.sps + 3) & ~3;
-    const int tiles = p.tiles_m * p.tiles_n;
-    const int units = tiles * p.splits;
-    const int G = gridDim.x;
-    // Workgroups are dispatched round-robin over the 8 XCDs (private L2s).
-    // With G % 8 == 0 the ids of one XCD are those with id % 8 == x; map
-    // them onto a contiguous range of units so that the units an XCD runs
-    // concurrently form a compact block of tiles (GROUP tile-rows tall).
-    const bool remap = (G & 7) == 0;
-    const int units8 = units & ~7;
-    auto unit_of = [&](int id) __attribute__((always_inline)) {
-        Unit u;
-        u.valid = id < units;
-        int x = min(id, units - 1);
-        if (remap && x < units8) x = (x & 7) * (units8 >> 3) + (x >> 3);
-        u.split = x / tiles;
-        const int t = x - u.split * tiles;
-        constexpr int GROUP = 8;
-        const int grp = t / (GROUP * p.tiles_n);
-        const int first_m = grp * GROUP;
-        const int gsz = min(p.tiles_m - first_m, GROUP);
-        const int tin = t - grp * GROUP * p.tiles_n;
-        u.m0 = (first_m + tin % gsz) * T::BM;
-        u.n0 = (tin / gsz) * T::BN;
-        u.sbeg = u.split * p.sps;
-        u.nst = min(p.sps, S_total - u.sbeg);
-        return u;
-    };
-
-    // Whole-operand resources; the unit's tile origin and the stage go into
-    // the scalar offset, a dead stage uses soffset = kOOB (reads zeros).
-    // The bounds keep every voffset + soffset below 2^32 (checked on the host).
-    const int Mpad = (p.M + 31) & ~31, Npad = (p.N + 31) & ~31;
-    const rsrc_t rA = make_rsrc(p.A, (uint32_t)(p.M * Kp));
-    const rsrc_t rB = make_rsrc(p.B, (uint32_t)(p.N * Kp));
-    const rsrc_t rAs = make_rsrc(p.As, (uint32_t)(Mpad * p.snp));
-    const rsrc_t rBs = make_rsrc(p.Bs, (uint32_t)(Npad * p.snp));
-    int sa[2][T::SA], sb[2][T::SB];  // scale dwords of two groups (set = group & 1)
-
-    // Per-lane offsets within a tile, fixed for the whole kernel.
-    // A DMA: fragment f, lane i -> row 16f + i%16, K-block i/16 of the stage.
-    uint32_t voA[T::DA];
-    static_for<T::DA>([&](auto d) {
-        voA[d] = (uint32_t)((16 * (w * T::DA + d) + (lane & 15)) * Kp + (lane >> 4) * 16);
-    });
-    // B: the wave's fragment j is 16 rows at n0 + wn*WN + 16j.
-    uint32_t voB[T::FN];
-    static_for<T::FN>([&](auto j) {
-        voB[j] = (uint32_t)((wn * T::FN + j) * K * 8 + lane * 16);
-    });
-    // Scale DMA i of this wave is the workgroup's DMA k = w + NW*i: k < NSDA
-    // gathers A chunks 4k..4k+3 (lane group lane/16 -> chunk), the next NSDB
-    // gather B chunks, any further k is a filler.  Lanes past the last chunk
-    // read out of range (0x7FFFFFF0 keeps voffset + soffset below 2^32).
-    uint32_t voSD[T::NSDW];
-    static_for<T::NSDW>([&](auto i) {
-        const int k = w + T::NW * i;
-        const int ch = 4 * (k < T::NSDA ? k : k - T::NSDA) + (lane >> 4);
-        const bool ok = k < T::NSDA ? ch < T::CA : (k < T::NSD && ch < T::CB);
-        voSD[i] = ok ? (uint32_t)(ch * 32 * p.snp + (lane & 15) * 16) : 0x7FFFFFF0u;
-    });
-    auto sbuf = [&](auto B) __attribute__((always_inline)) -> uint8_t* {
-        if constexpr ((decltype(B)::value & 1) == 0) return sc0;
-        else return sc1;
-    };
-    // DMA i of a scale group (target t: its unit and group) into buffer BUF.
-    auto scale_dma = [&](auto BUF, auto I, const auto& t) __attribute__((always_inline)) {
-        constexpr int i = decltype(I)::value;
-        const int k = w + T::NW * i;
-        if (k < T::NSD) {
-            const bool isa = k < T::NSDA;
-            dma16s(isa ? rAs : rBs, sbuf(BUF) + k * 1024, voSD[i], isa ? t.as : t.bs);
-        } else {
-            dma16s(rAs, fjunk, voSD[i], kOOB);
-        }
-    };
-    // This wave's scale dwords of the group in buffer BUF -> register set SET.
-    auto read_scales = [&](auto BUF, auto SET) __attribute__((always_inline)) {
-        constexpr int set = decltype(SET)::value;
-        static_for<T::SA>([&](auto i) {
-            sa[set][i] = *reinterpret_cast<const int*>(
-                sbuf(BUF) + (((wm * T::WM) >> 5) + i) * 256 + lane * 4);
-        });
-        static_for<T::SB>([&](auto j) {
-            sb[set][j] = *reinterpret_cast<const int*>(
-                sbuf(BUF) + T::NSDA * 1024 + (((wn * T::WN) >> 5) + j) * 256 + lane * 4);
-        });
-    };
-    const bool hi_lane = lane >= 32;
-    const uint32_t hi_bit = hi_lane ? kOOB : 0u;
-
-    i32x4 rb[4][T::FN];     // B register ring (stage % 4)
-    i32x4 ra[4];            // A fragment ring (fragment sequence % 4)
-    f32x4 acc[T::FM][T::FN];
-    static_for<T::FM>([&](auto i) {
-        static_for<T::FN>([&](auto j) { acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f}; });
-    });
-
-    Unit cur = unit_of(blockIdx.x);
-    Unit nxt = unit_of(blockIdx.x + G);
-
-    // Load target for local stage x of the current unit (x >= n_st4: stage
-    // x - n_st4 of the next unit).
-    struct Tgt {
-        uint32_t a, b, as, bs;  // scalar offsets (kOOB when dead)
-        uint32_t tv;            // per-lane K-tail bit (KTAIL only)
-    };
-    auto target = [&](int x) __attribute__((always_inline)) {
-        const bool in_cur = x < n_st4;
-        const int xl = in_cur ? x : x - n_st4;
-        const int m0 = in_cur ? cur.m0 : nxt.m0;
-        const int n0 = in_cur ? cur.n0 : nxt.n0;
-        const int sbeg = in_cur ? cur.sbeg : nxt.sbeg;
-        const int nst = in_cur ? cur.nst : nxt.nst;
-        const bool live = (in_cur || nxt.valid) && xl < nst;
-        const int s = sbeg + xl;
-        Tgt t;
-        t.a = live ? (uint32_t)(m0 * Kp + s * 64) : kOOB;
-        t.b = live ? (uint32_t)(n0 * Kp + s * 1024) : kOOB;
-        t.as = live ? (uint32_t)(m0 * p.snp + (s >> 1) * 256) : kOOB;
-        t.bs = live ? (uint32_t)(n0 * p.snp + (s >> 1) * 256) : kOOB;
-        t.tv = 0;
-        if constexpr (KTAIL) {
-            uint32_t v = ((uint32_t)(live && s == S_total - 1) << 31) & hi_bit;
-            asm volatile("" : "+v"(v));
-            t.tv = v;
-        }
-        return t;
-    };
-    // A fragment w*DA + d of a stage into its ring slot; when AF is not a
-    // multiple of the wave count, the surplus DMAs read out of range into
-    // fjunk, so every wave issues DA of them.
-    auto a_dma = [&](uint8_t* slot, auto D, const auto& t) __attribute__((always_inline)) {
-        constexpr int d = decltype(D)::value;
-        const int f = w * T::DA + d;
-        if (T::AF % T::NW == 0 || f < T::AF)
-            dma16s(rA, slot + f * 1024, voA[d] | t.tv, t.a);
-        else
-            dma16s(rA, fjunk, voA[d], kOOB);
-    };
-    // VMEM items issued at local stage ls (static slot u = ls & 3): DA
-    // A-DMAs and FN B-loads for stage ls+3 and, on odd stages, the NSDW scale
-    // DMAs of 256-K group (ls+3)/2 into buffer ((ls+3)/2) & 1.
-    auto issue_item = [&](auto U, auto D, const Tgt& t3) __attribute__((always_inline)) {
-        constexpr int u = decltype(U)::value;
-        constexpr int d = decltype(D)::value;
-        if constexpr (d < T::DA) {
-            a_dma(aslot(std::integral_constant<int, u + 3>{}), std::integral_constant<int, d>{}, t3);
-        } else if constexpr (d < T::DA + T::FN) {
-            constexpr int j = d - T::DA;
-            rb[(u + 3) & 3][j] = load16s(rB, voB[j] | t3.tv, t3.b);
-        } else {
-            scale_dma(std::integral_constant<int, ((u + 3) >> 1) & 1>{},
-                      std::integral_constant<int, d - T::DA - T::FN>{}, t3);
-        }
-    };
-    // Issues per stage: NI_EVEN on even stages, NI_ODD on odd ones.
-    constexpr int NI_EVEN = T::DA + T::FN;
-    constexpr int NI_ODD = T::DA + T::FN + T::NSDW;
-    // VMEM operations of an epilogue, all issued unconditionally: the bf16
-    // stores (one per fragment pair and row block) and the factor DMAs of the
-    // next unit (FD per wave).  vmcnt retires in issue order, so the first
-    // wait after an epilogue can leave them in flight (SPLIT: its fp32
-    // partial stores exceed the 6-bit count and are waited for).
-    constexpr int FD = T::NW == 1 ? 2 : 1;
-    constexpr int EPI_OPS = SPLIT ? 0 : T::FM * (T::FN / 2) + FD;
-    static_assert(NI_EVEN + EPI_OPS <= 63 && NI_ODD <= 63, "vmcnt is 6 bits");
-
-    // A fragment x of the stage in ring slot BUF -> register ra[R].
-    auto read_a = [&](auto BUF, auto X, auto R) __attribute__((always_inline)) {
-        ra[decltype(R)::value] = *reinterpret_cast<const i32x4*>(
-            aslot(BUF) + (wm * T::FM + decltype(X)::value) * 1024 + lane * 16);
-    };
-
-    // FIRST: the unit's first stage; its MFMAs start the accumulators from 0.
-    // `post`: stage of the first iteration of a unit that follows an
-    // epilogue.  Its u = 0 wait and barrier were done before that epilogue;
-    // its u = 1 wait also leaves the epilogue's EPI_OPS operations in flight.
-    auto stage = [&](auto U, auto FIRST, int ls, bool post) __attribute__((always_inline)) {
-        constexpr int u = decltype(U)::value;
-        constexpr bool first = decltype(FIRST)::value;
-        constexpr int h = u & 1, sset = (u >> 1) & 1;
-        constexpr int NI = ((u & 1) == 0) ? NI_EVEN : NI_ODD;   // issues of this stage
-        constexpr int NIP = ((u & 1) == 0) ? NI_ODD : NI_EVEN;  // issues of the previous one
-        constexpr int NCH = T::FM;
-        // Everything issued two or more stages ago has landed (A of ls+1 for
-        // this stage's look-ahead reads, B and scales of ls); the previous
-        // stage's issues may still be in flight.
-        if constexpr (u == 0) {
-            if (!post) {
-                wait_vmcnt<NIP>();
-                barrier();
-            }
-        } else if constexpr (u == 1) {
-            if (post) wait_vmcnt<NIP + EPI_OPS>();
-            else wait_vmcnt<NIP>();
-            barrier();
-        } else {
-            wait_vmcnt<NIP>();
-            barrier();
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        const Tgt t3 = target(ls + 3);
-        int sav[T::SA], sbv[T::SB];
-        static_for<T::SA>([&](auto i) { sav[i] = sa[sset][i]; });
-        static_for<T::SB>([&](auto j) { sbv[j] = sb[sset][j]; });
-        if constexpr (KTAIL) {
-            const bool tail = ls < cur.nst && cur.sbeg + ls == S_total - 1 && hi_lane;
-            static_for<T::SA>([&](auto i) { sav[i] = tail ? 0x7F7F7F7F : sav[i]; });
-            static_for<T::SB>([&](auto j) { sbv[j] = tail ? 0x7F7F7F7F : sbv[j]; });
-        }
-        static_for<NCH>([&](auto C) {
-            constexpr int c = decltype(C)::value;
-            // look-ahead A read: fragment c+2 of this stage or of the next
-            constexpr int xn = c + 2;
-            if constexpr (xn < T::FM)
-                read_a(std::integral_constant<int, u>{}, std::integral_constant<int, xn>{},
-                       std::integral_constant<int, (T::FM * u + xn) & 3>{});
-            else
-                read_a(std::integral_constant<int, u + 1>{},
-                       std::integral_constant<int, xn - T::FM>{},
-                       std::integral_constant<int, (T::FM * u + xn) & 3>{});
-            static_for<NI>([&](auto D) {
-                if constexpr (D * NCH / NI == c) issue_item(U, D, t3);
-            });
-            // Odd stages: read the next group's scales, DMA'd two stages ago.
-            if constexpr ((u & 1) == 1 && c == NCH / 2)
-                read_scales(std::integral_constant<int, ((u + 1) >> 1) & 1>{},
-                            std::integral_constant<int, ((u + 1) >> 1) & 1>{});
-            constexpr int ar = (T::FM * u + c) & 3;
-            static_for<T::FN>([&](auto j) {
-                constexpr int opb = (j & 1) + 2 * h;
-                constexpr int opa = (c & 1) + 2 * h;
-                // K-tail stages select scales with VALU ops: keep the wait states there.
-                if constexpr (first && !KTAIL)
-                    mfma_fp4_first<opb, opa>(acc[c][j], rb[u][j], ra[ar], sbv[j / 2], sav[c / 2]);
-                else
-                    mfma_fp4<opb, opa, KTAIL>(acc[c][j], rb[u][j], ra[ar], sbv[j / 2], sav[c / 2]);
-            });
-            __builtin_amdgcn_sched_barrier(0);
-        });
-    };
-
-    // MBS factors: bytes of a unit's rows and columns go to fbytes[par] by
-    // LDS DMA (wave 0: A, the last wave: B; a single wave does both).  Every
-    // wave issues exactly FD DMAs, the others (and every DMA without factors
-    // or past the last unit) read out of range into fjunk, so the count is
-    // the same for all waves and units.  The A range is cut to whole dwords;
-    // the at most 3 rows past it are read directly in the epilogue.
-    const bool has_f = (p.Af != nullptr) && (p.Bf != nullptr);
-    const int Mdw = p.M & ~3;
-    const rsrc_t rAf = make_rsrc(p.Af, has_f ? (uint32_t)Mdw : 0u);
-    const rsrc_t rBf = make_rsrc(p.Bf, has_f ? (uint32_t)p.N : 0u);
-    // Wave 0 loads the A bytes, wave NW-1-c the B chunk c (columns 256c..),
-    // every other wave a filler.
-    auto factor_dma = [&](const Unit& un, int par) __attribute__((always_inline)) {
-        const bool go = has_f && un.valid;
-        if constexpr (T::NW == 1) {
-            dma4s(rAf, &fbytes[par][0], (uint32_t)(un.m0 + lane * 4), go ? 0u : kOOB);
-            dma4s(rBf, &fbytes[par][256], (uint32_t)(un.n0 + lane * 4), go ? 0u : kOOB);
-        } else {
-            const bool wa = w == 0;
-            const int c = T::NW - 1 - w;            // B chunk of this wave
-            const bool wb = !wa && c < T::NBC;
-            uint8_t* dst = wa ? &fbytes[par][0] : (wb ? &fbytes[par][256 * (1 + c)] : fjunk);
-            const rsrc_t r = wa ? rAf : rBf;
-            const uint32_t off = (uint32_t)((wa ? un.m0 : un.n0 + 256 * c) + lane * 4);
-            dma4s(r, dst, off, go && (wa || wb) ? 0u : kOOB);
-        }
-    };
-    if (has_f) {
-        for (int b = threadIdx.x; b < 256; b += T::NT) ftab[b] = factor_of((uint32_t)b);
-    }
-    factor_dma(cur, 0);
-
-    // ---- prologue: scale groups 0 and 1, then stages 0..2 (A, B) of the first unit
-    static_for<2>([&](auto P) {
-        const Tgt t = target(2 * decltype(P)::value);
-        static_for<T::NSDW>([&](auto i) { scale_dma(P, i, t); });
-    });
-    static_for<3>([&](auto P) {
-        constexpr int ps = decltype(P)::value;
-        const Tgt t = target(ps);
-        static_for<T::DA>([&](auto d) {
-            a_dma(aslot(P), d, t);
-        });
-        static_for<T::FN>([&](auto j) { rb[ps][j] = load16s(rB, voB[j] | t.tv, t.b); });
-    });
-    // The first stage is entered as if stages "-2" and "-1" had run: wait
-    // for everything but stage 2's issues, then read the scales of group 0
-    // and A fragments 0 and 1.
-    wait_vmcnt<T::DA + T::FN>();
-    barrier();
-    read_scales(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
-    read_a(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{},
-           std::integral_constant<int, 0>{});
-    read_a(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{},
-           std::integral_constant<int, 1>{});
-
-    const int row_l = wm * T::WM + (lane & 15);
-    const int q = lane >> 4;
-    int par = 0;
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
-    using I3 = std::integral_constant<int, 3>;
-    using FT = std::integral_constant<bool, true>;
-    using FF = std::integral_constant<bool, false>;
-    for (int id = blockIdx.x; id < units; id += G) {
-        {   // first iteration, peeled: its stage 0 starts the accumulators
-            const bool post = id != (int)blockIdx.x;
-            if constexpr (KTAIL) {  // K-tail kernels keep plain MFMAs: zero first
-                static_for<T::FM>([&](auto i) {
-                    static_for<T::FN>([&](auto j) { acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f}; });
-                });
-            }
-            stage(I0{}, FT{}, 0, post);
-            stage(I1{}, FF{}, 1, post);
-            stage(I2{}, FF{}, 2, false);
-            stage(I3{}, FF{}, 3, false);
-        }
-        for (int ls0 = 4; ls0 < n_st4; ls0 += 4) {
-            stage(I0{}, FF{}, ls0, false);
-            stage(I1{}, FF{}, ls0 + 1, false);
-            stage(I2{}, FF{}, ls0 + 2, false);
-            stage(I3{}, FF{}, ls0 + 3, false);
-        }
-        // The next unit's first stage would wait and sync here; doing it now
-        // also makes this unit's factor bytes (and the table) visible.
-        wait_vmcnt<NI_ODD>();
-        barrier();
-        mfma_drain();
-
-        // ---- epilogue of unit `cur` -------------------------------------
-        const int rows_a = min(T::BM, p.M - cur.m0);
-        const int col_w = cur.n0 + wn * T::WN;
-        if constexpr (SPLIT) {
-            const rsrc_t rW = make_rsrc(p.ws + ((size_t)cur.split * p.M + cur.m0) * p.N,
-                                        (uint32_t)(rows_a * p.N * 4));
-            static_for<T::FN>([&](auto j) {
-                const int c = col_w + j * 16;
-                if (c < p.N) {
-                    static_for<T::FM>([&](auto i) {
-                        store16(rW, (uint32_t)(((row_l + i * 16) * p.N + c + q * 4) * 4), acc[i][j]);
-                    });
-                }
-            });
-        } else {
-            const rsrc_t rO = make_rsrc(p.out + (size_t)cur.m0 * p.N, (uint32_t)(rows_a * p.N * 2));
-            // HF: with MBS factors (out = C * (f(a_m) * f(b_n))); without them
-            // the accumulators are converted as they are.
-            auto epi = [&](auto HF) __attribute__((always_inline)) {
-                constexpr bool hf = decltype(HF)::value;
-                float fa[T::FM];
-                if constexpr (hf) {
-                    static_for<T::FM>([&](auto i) { fa[i] = ftab[fbytes[par][row_l + i * 16]]; });
-                    if (cur.m0 + T::BM > Mdw) {  // rows past the whole-dword range
-                        const rsrc_t rAf1 = make_rsrc(p.Af, (uint32_t)p.M);
-                        static_for<T::FM>([&](auto i) {
-                            const int r = cur.m0 + row_l + i * 16;
-                            if (r >= Mdw && r < p.M) fa[i] = factor_of(load1(rAf1, (uint32_t)r));
-                        });
-                    }
-                }
-                // Fragment pair (2p, 2p+1) covers 32 columns.  Lane (m, q) holds
-                // columns 4q..4q+3 of each; after the swaps it holds 8 consecutive
-                // columns 8q..8q+7 of the pair: a 16-byte store.  Stores are
-                // issued unconditionally (EPI_OPS): an out-of-range pair or half
-                // stores at kOOB, which the hardware drops.
-                static_for<T::FN / 2>([&](auto P2) {
-                    constexpr int j0 = 2 * decltype(P2)::value;
-                    const int c = col_w + j0 * 16;
-                    float f0[4], f1[4];
-                    if constexpr (hf) {
-                        const int cl = wn * T::WN + j0 * 16 + q * 4;
-                        const uint32_t b0 = *reinterpret_cast<const uint32_t*>(&fbytes[par][256 + cl]);
-                        const uint32_t b1 = *reinterpret_cast<const uint32_t*>(&fbytes[par][256 + cl + 16]);
-                        for (int k = 0; k < 4; ++k) {
-                            f0[k] = ftab[(b0 >> (8 * k)) & 255];
-                            f1[k] = ftab[(b1 >> (8 * k)) & 255];
-                        }
-                    }
-                    // N % 16 == 0: the pair is all in, only its first half, or out
-                    const bool store_ok = c < p.N && (c + 16 < p.N || q < 2);
-                    static_for<T::FM>([&](auto i) {
-                        f32x4 v0 = acc[i][j0], v1 = acc[i][j0 + 1];
-                        if constexpr (hf) {
-                            for (int k = 0; k < 4; ++k) {
-                                v0[k] = v0[k] * (fa[i] * f0[k]);
-                                v1[k] = v1[k] * (fa[i] * f1[k]);
-                            }
-                        }
-                        uint32_t x0 = pack_bf16x2(v0[0], v0[1]), x1 = pack_bf16x2(v0[2], v0[3]);
-                        uint32_t y0 = pack_bf16x2(v1[0], v1[1]), y1 = pack_bf16x2(v1[2], v1[3]);
-                        // round A: upper half of x <-> lower half of y
-                        auto a0 = __builtin_amdgcn_permlane32_swap(x0, y0, false, false);
-                        auto a1 = __builtin_amdgcn_permlane32_swap(x1, y1, false, false);
-                        // round B: odd rows of x <-> even rows of y
-                        auto b0s = __builtin_amdgcn_permlane16_swap(a0[0], a0[1], false, false);
-                        auto b1s = __builtin_amdgcn_permlane16_swap(a1[0], a1[1], false, false);
-                        const uint32_t o = (uint32_t)(((row_l + i * 16) * p.N + c + q * 8) * 2);
-                        i32x4 v = {(int)b0s[0], (int)b1s[0], (int)b0s[1], (int)b1s[1]};
-                        store16(rO, store_ok ? o : kOOB, __builtin_bit_cast(f32x4, v));
-                        // keep the accumulator reads of later blocks from being
-                        // hoisted here (register pressure)
-                        __builtin_amdgcn_sched_barrier(0);
-                    });
-                });
-            };
-            if (has_f) epi(std::true_type{});
-            else epi(std::false_type{});
-        }
-        par ^= 1;
-        factor_dma(nxt, par);
-        cur = nxt;
-        nxt = unit_of(id + 2 * G);
-    }
-    // The last unit prefetched dead stages into LDS and registers: let every
-    // transfer land before the workgroup's LDS is released.
-    wait_vmcnt<0>();
-}
-
-// ======================================================================
-// Skinny (decode) kernel: M <= 16*MT, MT in {1,2}
-// ======================================================================
-// A workgroup owns 16*NF rows of B (NF preshuffled 16-row fragments) and
-// NWK waves; wave kw owns a contiguous, 256-K aligned chunk of the K
-// stages and streams all NF fragments of it, so each A fragment it loads
-// (from L2: A is shared by every workgroup) feeds NF MFMAs.  B is read
-// once, with the non-temporal policy; up to U stages of B, A and scales
-// are in flight per wave.  Waves reduce their partial tiles through LDS
-// in a fixed order (deterministic), then NF*MT waves run the epilogue.
-template <int MT, int NF, int NWK, int U, bool SPLIT>
-__global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
-{
-    static_assert(U % 2 == 0, "batch must cover whole 256-K scale groups");
-    static_assert(NF == 1 || NF == 2, "one 32-row scale group per workgroup");
-    static_assert(NF * MT <= NWK, "one epilogue wave per output fragment");
-    __shared__ f32x4 red[NWK][NF * MT][64];
-
-    const int lane = threadIdx.x & 63;
-    const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n0 = blockIdx.x * 16 * NF;
-    const int split = blockIdx.y;
-
-    const int K = p.K, Kp = K >> 1;
-    const int S_total = (K + 127) >> 7;
-    const int s_begin = split * p.sps;
-    const int s_end = min(s_begin + p.sps, S_total);
-    const int n_st = s_end - s_begin;
-    const int CH = (((n_st + NWK - 1) / NWK) + 1) & ~1;
-    const int my_begin = s_begin + kw * CH;
-    const int my_end = min(my_begin + CH, s_end);
-
-    // B fragments beyond N read as zeros (range = valid fragments only).
-    const int nfrag = min(NF, (p.N - n0) >> 4);
-    const uint32_t fstride = (uint32_t)K * 8;  // bytes of one 16-row fragment column
-    const rsrc_t rB = make_rsrc(p.B + (size_t)(n0 >> 4) * fstride, (uint32_t)nfrag * fstride);
-    const rsrc_t rA = make_rsrc(p.A, (uint32_t)(p.M * Kp));
-    const rsrc_t rAs = make_rsrc(p.As, (uint32_t)(32 * p.snp));
-    const rsrc_t rBs = make_rsrc(p.Bs + (size_t)(n0 >> 5) * 32 * p.snp, (uint32_t)(32 * p.snp));
-    const bool hi_lane = lane >= 32;
-    const bool ktail = (K & 127) != 0;
-    // NF == 1: the workgroup's 16 rows are the low or high half of a 32-row
-    // scale group; shift that half's bytes into the op_sel 0/2 positions.
-    const int sshift = NF == 1 ? 8 * ((n0 >> 4) & 1) : 0;
-
-    f32x4 acc[NF][MT];
-    static_for<NF>([&](auto f) {
-        static_for<MT>([&](auto m) { acc[f][m] = f32x4{0.f, 0.f, 0.f, 0.f}; });
-    });
-
-    for (int st = my_begin; st < my_end; st += U) {
-        i32x4 b[U][NF], a[U][MT];
-        int sb[U / 2], sa[U / 2];
-        static_for<U>([&](auto u) {
-            const int s = st + u;
-            const bool ok = s < my_end;
-            const bool zap = (ktail && s == S_total - 1 && hi_lane) || !ok;
-            static_for<NF>([&](auto f) {
-                b[u][f] = load16nt(rB, zap ? kOOB : (uint32_t)(f * fstride + s * 1024 + lane * 16));
-            });
-            static_for<MT>([&](auto m) {
-                a[u][m] = load16(rA, zap ? kOOB
-                                         : (uint32_t)((16 * m + (lane & 15)) * Kp + s * 64 +
-                                                      (lane >> 4) * 16));
-            });
-        });
-        static_for<U / 2>([&](auto v) {
-            const int g = (st >> 1) + v;
-            const bool ok = st + 2 * v < my_end;
-            sb[v] = load4(rBs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
-            sa[v] = load4(rAs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
-        });
-        static_for<U>([&](auto u) {
-            constexpr int h = u & 1;
-            const int s = st + u;
-            int sbv = sb[u / 2] >> sshift;
-            int sav = sa[u / 2];
-            const bool tail = ktail && s == S_total - 1 && hi_lane;
-            sbv = tail ? 0x7F7F7F7F : sbv;
-            sav = tail ? 0x7F7F7F7F : sav;
-            static_for<NF>([&](auto f) {
-                static_for<MT>([&](auto m) {
-                    mfma_fp4<f + 2 * h, m + 2 * h>(acc[f][m], b[u][f], a[u][m], sbv, sav);
-                });
-            });
-        });
-    }
-
-    mfma_drain();
-    static_for<NF>([&](auto f) {
-        static_for<MT>([&](auto m) { red[kw][f * MT + m][lane] = acc[f][m]; });
-    });
-    __syncthreads();
-    if (kw >= NF * MT) return;
-    const int f = kw / MT, m = kw % MT;
-    if (n0 + 16 * f >= p.N) return;
-
-    f32x4 v = red[0][kw][lane];
-    for (int k = 1; k < NWK; ++k) v += red[k][kw][lane];
-    const int c = n0 + 16 * f + (lane >> 4) * 4;
-    const int row = 16 * m + (lane & 15);
-    if constexpr (SPLIT) {
-        const rsrc_t rW = make_rsrc(p.ws + (size_t)split * p.M * p.N, (uint32_t)(p.M * p.N * 4));
-        store16(rW, (uint32_t)((row * p.N + c) * 4), v);
-    } else {
-        if (p.Af && p.Bf) {
-            const rsrc_t rAf = make_rsrc(p.Af, (uint32_t)p.M);
-            const rsrc_t rBf = make_rsrc(p.Bf, (uint32_t)p.N);
-            const float fa = factor_of(load1(rAf, row));
-            const uint32_t bytes = (uint32_t)load4(rBf, c);
-            for (int q = 0; q < 4; ++q) v[q] = v[q] * (fa * factor_of(bytes >> (8 * q)));
-        }
-        const rsrc_t rO = make_rsrc(p.out, (uint32_t)(p.M * p.N * 2));
-        store8(rO, (uint32_t)((row * p.N + c) * 2), pack_bf16x2(v[0], v[1]),
-               pack_bf16x2(v[2], v[3]));
-    }
-}
+MBS_TILED_SHAPES(MBS_TILED_EXTERN)
+MBS_BDIRECT_SHAPES_A(MBS_BDIRECT_EXTERN)
+MBS_BDIRECT_SHAPES_B(MBS_BDIRECT_EXTERN)
+MBS_BDIRECT_SHAPES_C(MBS_BDIRECT_EXTERN)
+MBS_BDIRECT_SHAPES_D(MBS_BDIRECT_EXTERN)
+MBS_SKINNY_SHAPES(MBS_SKINNY_EXTERN)
 
 // ======================================================================
 // Split-K reduction: out[m][n..n+3] = epilogue(sum_s ws[s][m][n..n+3])
@@ -1024,67 +93,11 @@ struct Config {
     struct {
         float a, b, c;
     } cost;
-    // launch(args, grid, ktail, split, stream)
+    // launch(args, grid, general, split, stream); general: the K-tail variant
+    // (tiled kernels) or the dead-stage/K-tail variant (persistent kernels)
     hipError_t (*launch)(const GemmArgs&, dim3, bool, bool, hipStream_t);
     bool persistent = false;  // grid capped at the resident slots; workgroups loop over units
 };
-
-template <class T>
-hipError_t launch_tiled(const GemmArgs& a, dim3 grid, bool ktail, bool split, hipStream_t s)
-{
-    if (ktail) {
-        if (split) hipLaunchKernelGGL((gemm_tiled_kernel<T, true, true>), grid, dim3(T::NT), 0, s, a);
-        else hipLaunchKernelGGL((gemm_tiled_kernel<T, true, false>), grid, dim3(T::NT), 0, s, a);
-    } else {
-        if (split) hipLaunchKernelGGL((gemm_tiled_kernel<T, false, true>), grid, dim3(T::NT), 0, s, a);
-        else hipLaunchKernelGGL((gemm_tiled_kernel<T, false, false>), grid, dim3(T::NT), 0, s, a);
-    }
-    return hipGetLastError();
-}
-
-template <class T>
-hipError_t launch_bdirect(const GemmArgs& a, dim3 grid, bool ktail, bool split, hipStream_t s)
-{
-    if (ktail) {
-        if (split) hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, true>), grid, dim3(T::NT), 0, s, a);
-        else hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false>), grid, dim3(T::NT), 0, s, a);
-    } else {
-        if (split) hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, true>), grid, dim3(T::NT), 0, s, a);
-        else hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false>), grid, dim3(T::NT), 0, s, a);
-    }
-    return hipGetLastError();
-}
-
-template <int MT, int NF, int NWK, int U>
-hipError_t launch_skinny(const GemmArgs& a, dim3 grid, bool, bool split, hipStream_t s)
-{
-    if (split) hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, true>), grid, dim3(64 * NWK), 0, s, a);
-    else hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, false>), grid, dim3(64 * NWK), 0, s, a);
-    return hipGetLastError();
-}
-
-using T256x256 = TileShape<256, 256, 2, 2>;
-using T256x128 = TileShape<256, 128, 2, 2>;
-using T128x256 = TileShape<128, 256, 2, 2>;
-using T128x128 = TileShape<128, 128, 2, 2>;
-using T64x256 = TileShape<64, 256, 1, 4>;
-using T64x128 = TileShape<64, 128, 1, 2>;
-using T64x64 = TileShape<64, 64, 1, 1>;
-
-using B256x256 = BdShape<256, 256, 2, 2>;
-using B256x128 = BdShape<256, 128, 2, 2>;
-using B128x256 = BdShape<128, 256, 2, 2>;
-using B128x128 = BdShape<128, 128, 2, 2>;
-using B64x256 = BdShape<64, 256, 1, 4>;
-using B64x128 = BdShape<64, 128, 1, 2>;
-using B64x64 = BdShape<64, 64, 1, 1>;
-using B256x256w14 = BdShape<256, 256, 1, 4>;
-using B192x256w14 = BdShape<192, 256, 1, 4>;
-using B96x256w14 = BdShape<96, 256, 1, 4>;
-using B64x512w14 = BdShape<64, 512, 1, 4>;
-using B128x384w14 = BdShape<128, 384, 1, 4>;
-using B256x128w14 = BdShape<256, 128, 1, 4>;
-using B128x256w14 = BdShape<128, 256, 1, 4>;
 
 const Config kConfigs[] = {
     {"tiled_256x256_w2x2", kTiled, 256, 256, 256, 1, {0.703f, 0.703f, 3.99f}, launch_tiled<T256x256>},
@@ -1274,7 +287,7 @@ int validate(const uint8_t* A, const uint8_t* B, const uint8_t* As, const uint8_
         return fail(MBS_ERR_ARGUMENT, "Mpad must be round_up(M, 32)");
     if (snp != ((K + 31) / 32 + 7) / 8 * 8)
         return fail(MBS_ERR_ARGUMENT, "scaleN_pad must be round_up(ceil(K/32), 8)");
-    if ((int64_t)256 * (K / 2) >= (1ll << 31) || (int64_t)256 * N * 4 >= (1ll << 31) ||
+    if ((int64_t)512 * (K / 2) + 4096 >= (1ll << 31) || (int64_t)256 * N * 4 >= (1ll << 31) ||
         (int64_t)M * (K / 2) >= (1ll << 31) || (int64_t)N * (K / 2) >= (1ll << 31) ||
         (int64_t)M * N * 4 >= (1ll << 31))
         return fail(MBS_ERR_ARGUMENT, "problem too large for 32-bit buffer offsets");
@@ -1300,7 +313,14 @@ int run_plan(const Plan& pl, const uint8_t* A, const uint8_t* B, const uint8_t* 
     a.sps = pl.sps;
     hipStream_t s = static_cast<hipStream_t>(stream);
     (void)hipGetLastError();  // do not report a stale error as ours
-    hipError_t e = c.launch(a, pl.grid, (K % 128) != 0, pl.splits > 1, s);
+    // Persistent kernels take their general variant when a unit can have
+    // dead stages (a split shorter than the others, or a stage count that is
+    // not a multiple of 4) or K has a 64-wide tail; the others, their
+    // constant-step variant.
+    const int S_total = stages_of(K);
+    const bool ktail = (K % 128) != 0;
+    const bool gen = c.persistent ? (ktail || pl.sps % 4 != 0 || S_total % pl.sps != 0) : ktail;
+    hipError_t e = c.launch(a, pl.grid, gen, pl.splits > 1, s);
     if (e != hipSuccess) return fail(MBS_ERR_LAUNCH, std::string("launch failed: ") + hipGetErrorString(e));
     if (pl.splits > 1) {
         const int64_t quads = (int64_t)M * (N / 4);

@@ -194,6 +194,17 @@ __device__ __forceinline__ void mfma_drain()
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 }
 
+// Orders every later read of `acc` after an mfma_drain(): the empty asm
+// "rewrites" the accumulator, so the AGPR->VGPR copies the compiler makes
+// for its readers depend on it, and volatile asm statements keep their
+// relative order.  Without it the scheduler may hoist those copies above
+// the drain (it cannot see the latency of an MFMA written as inline asm)
+// and read an accumulator an MFMA is still writing.
+__device__ __forceinline__ void pin_after_drain(f32x4& acc)
+{
+    asm volatile("" : "+a"(acc));
+}
+
 // ----------------------------------------------------------- MBS factor
 // f(b) = 1/(1+b/256) = 256/(256+b), correctly rounded to fp32, computed at
 // compile time with integer long division (no run-time division needed).
