@@ -125,6 +125,26 @@ int mbs_shuffle_b(const uint8_t* w, uint8_t* out, int N, int K, void* stream);
 int mbs_shuffle_scales(const uint8_t* plain, uint8_t* out, int rows, int K, int pad_byte,
                        void* stream);
 
+/* Inverse of mbs_shuffle_b: (16,16)-preshuffled [N, K/2] -> plain [N, K/2]
+ * (out of place).  The inverse of aiter.ops.shuffle.shuffle_weight, which
+ * the reference does not have; used to read back the on-disk weight format
+ * (test_gemm_a4w4.py:141 produces it). */
+int mbs_unshuffle_b(const uint8_t* in, uint8_t* w, int N, int K, void* stream);
+
+/* Inverse of mbs_shuffle_scales on the live entries: shuffled buffer ->
+ * plain [rows, K/32] (the padding is dropped).  K % 32 == 0. */
+int mbs_unshuffle_scales(const uint8_t* shuffled, uint8_t* plain, int rows, int K, void* stream);
+
+/* Format check of a shuffled scale buffer (round_up(rows,32)*scaleN_pad
+ * bytes): writes counts[0] = padding entries != pad_byte (pad_byte = -1
+ * skips that check) and counts[1] = live entries equal to 0xFF (E8M0 NaN).
+ * `counts` is 2 device uint32 words, written (not accumulated), so it needs
+ * no clearing.  One workgroup: meant for load-time validation, not the hot
+ * path.  No counterpart in the reference, whose launcher reads the buffer
+ * unchecked (interface/gemm_a4w4_pybind.cpp:22-44 checks no scale size). */
+int mbs_check_scales(const uint8_t* shuffled, int rows, int K, int pad_byte, uint32_t* counts,
+                     void* stream);
+
 /* Packed operand + shuffled scales -> fp32 [rows, K]:
  * e2m1(code) * 2^(e-127) (e=255 -> NaN).  b_preshuffled selects the B layout
  * for `packed`.  Replaces fp4_utils.mxfp4_to_f32 * e8m0_to_f32 as used by

@@ -94,6 +94,22 @@ def dequant_mxfp4(packed, scale, b_preshuffled: bool = False):
     return ext().dequant_mxfp4(packed, scale, b_preshuffled)
 
 
+def unshuffle_weight(b):
+    """Inverse of ``shuffle_weight``: preshuffled [N,K/2] -> plain [N,K/2]."""
+    return ext().unshuffle_weight(b)
+
+
+def unshuffle_scales(s, rows: int, K: int):
+    """Shuffled E8M0 buffer -> plain [rows, K/32] (padding dropped)."""
+    return ext().unshuffle_scales(s, rows, K)
+
+
+def check_scales(s, rows: int, K: int, pad_byte: int = 127):
+    """(padding bytes != pad_byte, live 0xFF bytes) of a shuffled scale buffer;
+    ``pad_byte=-1`` skips the padding check.  Synchronises."""
+    return ext().check_scales(s, rows, K, pad_byte)
+
+
 def scale_pad(K: int) -> int:
     """scaleN_pad = round_up(ceil(K/32), 8)."""
     return ((K + 31) // 32 + 7) // 8 * 8

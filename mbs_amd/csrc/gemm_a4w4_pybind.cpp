@@ -223,6 +223,56 @@ at::Tensor shuffle_scales(at::Tensor s, int64_t pad_byte)
     return out;
 }
 
+// (16,16)-preshuffled weights [N, K/2] -> plain copy (inverse of shuffle_weight).
+at::Tensor unshuffle_weight(at::Tensor b)
+{
+    TORCH_CHECK(b.is_cuda() && b.dim() == 2 && b.element_size() == 1,
+                "unshuffle_weight: b must be a 2D 1-byte device tensor");
+    auto bu = as_bytes(b);
+    c10::DeviceGuard guard(b.device());
+    auto out = torch::empty_like(bu);
+    check_status(mbs_unshuffle_b(bu.data_ptr<uint8_t>(), out.data_ptr<uint8_t>(), (int)bu.size(0),
+                                 (int)(bu.size(1) * 2), current_stream(b)),
+                 "unshuffle_weight");
+    return out;
+}
+
+// Shuffled E8M0 buffer of `rows` rows -> plain [rows, K/32] (inverse of shuffle_scales).
+at::Tensor unshuffle_scales(at::Tensor s, int64_t rows, int64_t K)
+{
+    TORCH_CHECK(s.is_cuda() && s.element_size() == 1,
+                "unshuffle_scales: s must be a 1-byte device tensor");
+    TORCH_CHECK(rows >= 1 && K >= 32 && K % 32 == 0, "unshuffle_scales: need rows >= 1, K % 32 == 0");
+    auto su = as_bytes(s);
+    TORCH_CHECK(su.numel() >= round_up(rows, 32) * scale_pad(K), "unshuffle_scales: buffer too small");
+    c10::DeviceGuard guard(s.device());
+    auto out = torch::empty({rows, K / 32}, torch::TensorOptions().dtype(torch::kByte).device(s.device()));
+    check_status(mbs_unshuffle_scales(su.data_ptr<uint8_t>(), out.data_ptr<uint8_t>(), (int)rows,
+                                      (int)K, current_stream(s)),
+                 "unshuffle_scales");
+    return out;
+}
+
+// Format check of a shuffled scale buffer: (padding entries != pad_byte,
+// live entries equal to 0xFF).  pad_byte = -1 skips the padding check.
+// Synchronises the stream (load-time validation, not the hot path).
+std::tuple<int64_t, int64_t> check_scales(at::Tensor s, int64_t rows, int64_t K, int64_t pad_byte)
+{
+    TORCH_CHECK(s.is_cuda() && s.element_size() == 1,
+                "check_scales: s must be a 1-byte device tensor");
+    TORCH_CHECK(rows >= 1 && K >= 32 && K % 32 == 0, "check_scales: need rows >= 1, K % 32 == 0");
+    auto su = as_bytes(s);
+    TORCH_CHECK(su.numel() >= round_up(rows, 32) * scale_pad(K), "check_scales: buffer too small");
+    c10::DeviceGuard guard(s.device());
+    auto counts = torch::empty({2}, torch::TensorOptions().dtype(torch::kInt32).device(s.device()));
+    check_status(mbs_check_scales(su.data_ptr<uint8_t>(), (int)rows, (int)K, (int)pad_byte,
+                                  reinterpret_cast<uint32_t*>(counts.data_ptr<int32_t>()),
+                                  current_stream(s)),
+                 "check_scales");
+    auto h = counts.cpu();
+    return {(int64_t)(uint32_t)h[0].item<int32_t>(), (int64_t)(uint32_t)h[1].item<int32_t>()};
+}
+
 // Packed operand + shuffled scales -> fp32 [R, K] (mxfp4_to_f32 * e8m0_to_f32).
 at::Tensor dequant_mxfp4(at::Tensor packed, at::Tensor scale_shuffled, bool b_preshuffled)
 {
@@ -270,6 +320,13 @@ PYBIND11_MODULE(mbs_gemm_a4w4, m)
     m.def("shuffle_weight", &shuffle_weight, "(16,16) preshuffle of packed weights",
           pybind11::arg("w"));
     m.def("shuffle_scales", &shuffle_scales, "plain -> shuffled E8M0 scales", pybind11::arg("s"),
+          pybind11::arg("pad_byte") = 127);
+    m.def("unshuffle_weight", &unshuffle_weight, "inverse of shuffle_weight", pybind11::arg("b"));
+    m.def("unshuffle_scales", &unshuffle_scales, "shuffled -> plain E8M0 scales [rows, K/32]",
+          pybind11::arg("s"), pybind11::arg("rows"), pybind11::arg("K"));
+    m.def("check_scales", &check_scales,
+          "(padding entries != pad_byte, live 0xFF entries) of a shuffled scale buffer",
+          pybind11::arg("s"), pybind11::arg("rows"), pybind11::arg("K"),
           pybind11::arg("pad_byte") = 127);
     m.def("dequant_mxfp4", &dequant_mxfp4, "packed + shuffled scales -> fp32",
           pybind11::arg("packed"), pybind11::arg("scale"), pybind11::arg("b_preshuffled") = false);

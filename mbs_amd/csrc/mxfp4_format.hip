@@ -195,6 +195,66 @@ shuffle_b_kernel(const uint8_t* __restrict__ w, uint8_t* __restrict__ out, int N
         *reinterpret_cast<const i32x4*>(w + (int64_t)n * Kp + kp);
 }
 
+// Inverse of shuffle_b_kernel: preshuffled [N, K/2] -> plain row-major.
+__global__ void __launch_bounds__(256)
+unshuffle_b_kernel(const uint8_t* __restrict__ in, uint8_t* __restrict__ w, int N, int Kp)
+{
+    const int per_row = Kp >> 4;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)N * per_row) return;
+    const int n = (int)(i / per_row), kp = (int)(i - (int64_t)n * per_row) * 16;
+    *reinterpret_cast<i32x4*>(w + (int64_t)n * Kp + kp) =
+        *reinterpret_cast<const i32x4*>(in + flat_b(n, kp, Kp));
+}
+
+// Inverse of shuffle_scales_kernel on the live entries: shuffled -> plain
+// [rows, nb] (the padding is dropped).
+__global__ void __launch_bounds__(256)
+unshuffle_scales_kernel(const uint8_t* __restrict__ sshuf, uint8_t* __restrict__ plain, int rows,
+                        int nb, int snp)
+{
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)rows * nb) return;
+    const int r = (int)(i / nb), b = (int)(i - (int64_t)r * nb);
+    plain[i] = sshuf[flat_s(r, b, snp)];
+}
+
+// Format check of a shuffled scale buffer, one workgroup (no atomics, so the
+// counts need no clearing): counts[0] = padding entries that differ from
+// `pad` (pad < 0: not checked), counts[1] = live entries equal to 0xFF (the
+// E8M0 NaN encoding, which turns a whole block of the product into NaN).
+__global__ void __launch_bounds__(1024)
+check_scales_kernel(const uint8_t* __restrict__ sshuf, int rows, int nb, int snp, int pad,
+                    uint32_t* __restrict__ counts)
+{
+    __shared__ uint32_t part[2][16];
+    const int rows_pad = (rows + 31) & ~31;
+    const int64_t total = (int64_t)rows_pad * snp;
+    uint32_t bad_pad = 0, nan_live = 0;
+    for (int64_t i = threadIdx.x; i < total; i += 1024) {
+        const int r = (int)(i / snp), b = (int)(i - (int64_t)r * snp);
+        const uint32_t v = sshuf[flat_s(r, b, snp)];
+        const bool live = r < rows && b < nb;
+        bad_pad += (!live && pad >= 0 && v != (uint32_t)pad) ? 1u : 0u;
+        nan_live += (live && v == 0xFFu) ? 1u : 0u;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        bad_pad += __shfl_xor(bad_pad, o);
+        nan_live += __shfl_xor(nan_live, o);
+    }
+    const int wv = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        part[0][wv] = bad_pad;
+        part[1][wv] = nan_live;
+    }
+    __syncthreads();
+    if (threadIdx.x < 2) {
+        uint32_t t = 0;
+        for (int k = 0; k < 16; ++k) t += part[threadIdx.x][k];
+        counts[threadIdx.x] = t;
+    }
+}
+
 // fp32 bits of (code value) * 2^(e-127), built with integer ops so the result
 // is exact whatever the float denormal mode: the code value is k/2 with k in
 // {0,1,2,3,4,6,8,12}, so the product is k * 2^(e-128).
@@ -329,6 +389,41 @@ int mbs_shuffle_scales(const uint8_t* plain, uint8_t* out, int rows, int K, int 
     hipLaunchKernelGGL(shuffle_scales_kernel, dim3(blocks_for(n)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), plain, out, rows, K / 32, snp,
                        (uint8_t)pad_byte);
+    return launched();
+}
+
+int mbs_unshuffle_b(const uint8_t* in, uint8_t* w, int N, int K, void* stream)
+{
+    if (!in || !w) return fmt_fail("null pointer");
+    if (N < 16 || N % 16 || K < 64 || K % 64) return fmt_fail("need N % 16 == 0 and K % 64 == 0");
+    if (in == w) return fmt_fail("unshuffle_b is out of place");
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(unshuffle_b_kernel, dim3(blocks_for((int64_t)N * (K / 32))), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), in, w, N, K / 2);
+    return launched();
+}
+
+int mbs_unshuffle_scales(const uint8_t* shuffled, uint8_t* plain, int rows, int K, void* stream)
+{
+    if (!shuffled || !plain) return fmt_fail("null pointer");
+    if (rows < 1 || K < 32 || K % 32) return fmt_fail("need rows >= 1 and K % 32 == 0");
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(unshuffle_scales_kernel, dim3(blocks_for((int64_t)rows * (K / 32))),
+                       dim3(256), 0, static_cast<hipStream_t>(stream), shuffled, plain, rows,
+                       K / 32, scale_pad_of(K));
+    return launched();
+}
+
+int mbs_check_scales(const uint8_t* shuffled, int rows, int K, int pad_byte, uint32_t* counts,
+                     void* stream)
+{
+    if (!shuffled || !counts) return fmt_fail("null pointer");
+    if (rows < 1 || K < 32 || K % 32) return fmt_fail("need rows >= 1 and K % 32 == 0");
+    if (pad_byte < -1 || pad_byte > 255) return fmt_fail("pad_byte must be a byte or -1");
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(check_scales_kernel, dim3(1), dim3(1024), 0,
+                       static_cast<hipStream_t>(stream), shuffled, rows, K / 32, scale_pad_of(K),
+                       pad_byte, counts);
     return launched();
 }
 
