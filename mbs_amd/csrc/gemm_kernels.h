@@ -333,12 +333,14 @@ __global__ void __launch_bounds__(T::NT) gemm_tiled_kernel(const GemmArgs p)
 // the preshuffled B is already in MFMA fragment order (one 1-KiB
 // contiguous block per 16 rows x 128 K), so each wave loads its B fragments
 // with plain 16-byte buffer loads straight into VGPRs, three stages ahead,
-// into a 4-deep register ring.  Scale dwords (one per lane per 32-row group
-// and 256-K group) are likewise loaded straight into VGPRs.  This halves the
-// LDS traffic of the stage (LDS bandwidth, not the MFMA pipe, is what limits
-// the all-LDS design), and A fragments are read from LDS just in time, two
-// MFMA rows ahead.  The epilogue turns each pair of 16-column fragments into
-// 16-byte row segments with two rounds of permlane swaps before storing.
+// into a 4-deep register ring.  This halves the LDS traffic of the stage
+// (LDS bandwidth, not the MFMA pipe, is what limits the all-LDS design).
+// A moves through LDS in 256-K "pairs" (two 128-K stages, 128 bytes of each
+// row: whole cache lines, so every DMA instruction fetches 8 full lines
+// instead of 16 half lines), in a ring of three pair slots; each slot row is
+// 8 16-byte chunks stored XOR-swizzled so that the MFMA fragment reads are
+// bank-conflict free.  The epilogue turns each pair of 16-column fragments
+// into 16-byte row segments with two rounds of permlane swaps.
 template <int BM_, int BN_, int WGM_, int WGN_>
 struct BdShape {
     static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
@@ -346,9 +348,11 @@ struct BdShape {
     static constexpr int WM = BM / WGM, WN = BN / WGN;
     static constexpr int FM = WM / 16, FN = WN / 16;
     static constexpr int AF = BM / 16;                  // A fragments per stage
-    static constexpr int DA = (AF + NW - 1) / NW;       // A DMAs per wave per stage
+    // A DMAs per stage: half a pair (BM/2 rows x 128 bytes, 8 rows each),
+    // DA per wave.
+    static constexpr int DA = (AF + NW - 1) / NW;
     static constexpr int SA = FM / 2, SB = FN / 2;      // scale dwords per wave per group
-    static constexpr int ASLOT = AF * 1024;             // bytes of one A ring slot
+    static constexpr int PSLOT = BM * 128;              // bytes of one A pair slot
     // Scales of a 256-K group: one 256-byte chunk per 32 rows (A) or columns
     // (B), gathered four chunks per 16-byte LDS DMA.
     static constexpr int CA = BM / 32, CB = BN / 32;
@@ -362,7 +366,8 @@ struct BdShape {
     static constexpr int FBW = 256 * (1 + NBC);
     static_assert(BM <= 256, "one 256-byte chunk of A factor bytes");
     static_assert(NW == 1 ? NBC == 1 : NW >= 1 + NBC, "one factor DMA per wave");
-    static_assert(4 * ASLOT + 2 * SBUF <= 150 * 1024, "LDS budget");
+    static_assert(BM % 32 == 0, "pair halves of whole 16-row groups (swizzle parity)");
+    static_assert(3 * PSLOT + 2 * SBUF <= 150 * 1024, "LDS budget");
 };
 
 // One work unit of the persistent schedule (a tile and a K-split of it);
@@ -374,21 +379,37 @@ struct Unit {
     int valid;     // 0: past the end of this workgroup's unit list
 };
 
+// Chunk swizzle of an A pair slot: row r keeps its global 16-byte chunk c at
+// physical chunk c ^ swz(r).  Any 8 consecutive rows (and, per row parity,
+// any 16) then spread a fragment read (16 rows, one chunk) over all banks.
+__device__ __forceinline__ int a_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
 // Persistent B-direct kernel: gridDim.x workgroups (at most one resident
 // set per CU) walk work units id = blockIdx.x + i*gridDim.x.  Per unit the
 // K loop runs n_st4 = round_up(sps, 4) stages (stages past the split end are
 // dead: their loads read zeros).  The software pipeline crosses unit
 // boundaries: the last four stages of a unit already prefetch the next
-// unit's first three stages and scale group, so the next unit's MFMAs start
-// right after this unit's epilogue, and no workgroup relaunch (with its
-// pipeline fill and store drain) happens between tiles.
+// unit's first stages and scale group, so the next unit's MFMAs start right
+// after this unit's epilogue, and no workgroup relaunch (with its pipeline
+// fill and store drain) happens between tiles.
+//
+// Schedule of a stage ls (u = ls & 3): MFMAs of stage ls; loads of B stage
+// ls+3 and (odd ls) scale group (ls+3)/2; the A DMA of half (ls & 1) of the
+// pair starting at stage (ls & ~1) + 4.  A pair slot is rewritten only after
+// the barrier that follows the last read of its previous pair, and the
+// stage-top wait (everything issued two or more stages ago has landed)
+// covers every pair before its first read, with three slots.  The slot of a
+// pair is its running index mod 3 across units: the three slot pointers
+// rotate by one position per 4-stage iteration (two pairs).  A fragment and
+// scale reads are explicit ds_read instructions with counted lgkmcnt waits
+// (the compiler would otherwise make them wait for the A DMA into the
+// dynamically chosen slot).
 template <class T, bool GEN, bool SPLIT>
 __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
 {
-    __shared__ __attribute__((aligned(1024))) uint8_t sa0[T::ASLOT];
-    __shared__ __attribute__((aligned(1024))) uint8_t sa1[T::ASLOT];
-    __shared__ __attribute__((aligned(1024))) uint8_t sa2[T::ASLOT];
-    __shared__ __attribute__((aligned(1024))) uint8_t sa3[T::ASLOT];
+    __shared__ __attribute__((aligned(1024))) uint8_t pa0[T::PSLOT];
+    __shared__ __attribute__((aligned(1024))) uint8_t pa1[T::PSLOT];
+    __shared__ __attribute__((aligned(1024))) uint8_t pa2[T::PSLOT];
     // MBS factor bytes of a unit (A rows at [0,256), B columns at [256,512)),
     // double-buffered by unit parity, and the byte -> fp32 factor table.
     __shared__ __attribute__((aligned(16))) uint8_t fbytes[2][T::FBW];
@@ -397,12 +418,17 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     __shared__ __attribute__((aligned(1024))) uint8_t sc0[T::SBUF];
     __shared__ __attribute__((aligned(1024))) uint8_t sc1[T::SBUF];
     __shared__ float ftab[256];
-    auto aslot = [&](auto B) __attribute__((always_inline)) -> uint8_t* {
-        constexpr int b = decltype(B)::value & 3;
-        if constexpr (b == 0) return sa0;
-        else if constexpr (b == 1) return sa1;
-        else if constexpr (b == 2) return sa2;
-        else return sa3;
+    // Pair slots of the current 4-stage iteration: q0 (pair 0, stages 0-1),
+    // q1 (pair 1, stages 2-3), q2 (pair 2, DMA'd by stages 0-1); pair 3 (DMA'd
+    // by stages 2-3) reuses q0.  Next iteration: (q0, q1, q2) <- (q2, q0, q1).
+    uint8_t* q0 = pa0;
+    uint8_t* q1 = pa1;
+    uint8_t* q2 = pa2;
+    auto qp = [&](auto K) __attribute__((always_inline)) -> uint8_t* {
+        constexpr int k = decltype(K)::value & 3;
+        if constexpr (k == 0 || k == 3) return q0;
+        else if constexpr (k == 1) return q1;
+        else return q2;
     };
 
     const int lane = threadIdx.x & 63;
@@ -451,10 +477,23 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     int sa[2][T::SA], sb[2][T::SB];  // scale dwords of two groups (set = group & 1)
 
     // Per-lane offsets within a tile, fixed for the whole kernel.
-    // A DMA: fragment f, lane i -> row 16f + i%16, K-block i/16 of the stage.
-    uint32_t voA[T::DA];
+    // A DMA j of a pair half: lane i -> row 8j + i/8 of the half, physical
+    // chunk i%8, which holds global chunk (i%8) ^ swz(row); swz(row) =
+    // (i/8) ^ (j & 1) since the half starts at a multiple of 16 rows.
+    // cA: the lane's K-byte offset in the pair (K-tail and dead-stage masks).
+    uint32_t voA[T::DA], cA[T::DA];
     static_for<T::DA>([&](auto d) {
-        voA[d] = (uint32_t)((16 * (w * T::DA + d) + (lane & 15)) * Kp + (lane >> 4) * 16);
+        const int j = w * T::DA + d;
+        const int c = (lane & 7) ^ (lane >> 3) ^ (j & 1);
+        cA[d] = (uint32_t)(c * 16);
+        voA[d] = (uint32_t)((8 * j + (lane >> 3)) * Kp + c * 16);
+    });
+    // A fragment read of half h: lane L -> row L%16 of the fragment, global
+    // chunk 4h + L/16, at its swizzled position.
+    uint32_t loA[2];
+    static_for<2>([&](auto H) {
+        constexpr int h = decltype(H)::value;
+        loA[h] = (uint32_t)((lane & 15) * 128 + (((4 * h + (lane >> 4)) ^ a_swz(lane & 15)) * 16));
     });
     // B: the wave's fragment j is 16 rows at n0 + wn*WN + 16j.
     uint32_t voB[T::FN];
@@ -489,18 +528,13 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         uint8_t* dst = real ? sbuf(BUF) + k * 1024 : fjunk;
         dma16s(isa ? rAs : rBs, dst, voSD[i], real ? (isa ? t.as : t.bs) : kOOB);
     };
-    // This wave's scale dwords of the group in buffer BUF -> register set SET.
-    auto read_scales = [&](auto BUF, auto SET) __attribute__((always_inline)) {
-        constexpr int set = decltype(SET)::value;
-        static_for<T::SA>([&](auto i) {
-            sa[set][i] = *reinterpret_cast<const int*>(
-                sbuf(BUF) + (((wm * T::WM) >> 5) + i) * 256 + lane * 4);
-        });
-        static_for<T::SB>([&](auto j) {
-            sb[set][j] = *reinterpret_cast<const int*>(
-                sbuf(BUF) + T::NSDA * 1024 + (((wn * T::WN) >> 5) + j) * 256 + lane * 4);
-        });
-    };
+    // LDS addresses of this wave's scale dwords in each scale buffer (dword
+    // k of the A or B part at + k*256).
+    const uint32_t scA[2] = {lds_addr(sc0) + (uint32_t)((((wm * T::WM) >> 5)) * 256 + lane * 4),
+                             lds_addr(sc1) + (uint32_t)((((wm * T::WM) >> 5)) * 256 + lane * 4)};
+    const uint32_t scB[2] = {
+        lds_addr(sc0) + (uint32_t)(T::NSDA * 1024 + ((wn * T::WN) >> 5) * 256 + lane * 4),
+        lds_addr(sc1) + (uint32_t)(T::NSDA * 1024 + ((wn * T::WN) >> 5) * 256 + lane * 4)};
     // GEN kernels also run shapes without a K tail (dead stages only).
     const bool ktail = (K & 127) != 0;
     const bool hi_lane = lane >= 32;
@@ -559,25 +593,49 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         }
         return t;
     };
-    // A fragment w*DA + d of a stage into its ring slot; when AF is not a
-    // multiple of the wave count, the surplus DMAs read out of range into
-    // fjunk, so every wave issues DA of them.
-    auto a_dma = [&](uint8_t* slot, auto D, const auto& t) __attribute__((always_inline)) {
-        constexpr int d = decltype(D)::value;
-        const int f = w * T::DA + d;
-        if (T::AF % T::NW == 0 || f < T::AF)
-            dma16s(rA, slot + f * 1024, voA[d] | t.tv, t.a);
+    // A DMA w*DA + d of half H of pair K (of the iteration) into its slot.  `soff`: the
+    // pair's scalar offset (kOOB + small when dead); GEN kernels also mask
+    // the lanes whose chunk lies past the pair's `vb` live bytes (K tail,
+    // dead stage).  When AF is not a multiple of the wave count, the surplus
+    // DMAs read out of range into fjunk, so every wave issues DA of them.
+    auto a_dma = [&](auto PK, auto H, auto D, uint32_t soff, int vb) __attribute__((always_inline)) {
+        constexpr int d = decltype(D)::value, h = decltype(H)::value;
+        const int j = w * T::DA + d;
+        uint32_t vo = voA[d];
+        if constexpr (GEN) vo |= ((int)cA[d] >= vb) ? kOOB : 0u;
+        const uint32_t so = soff + (uint32_t)(h * (T::BM / 2) * Kp);
+        if (T::AF % T::NW == 0 || j < T::AF)
+            dma16s(rA, qp(PK) + h * (T::BM / 2) * 128 + j * 1024, vo, so);
         else
             dma16s(rA, fjunk, voA[d], kOOB);
+    };
+    // Scalar offset and live bytes of the A pair DMA'd at local stage ls
+    // (the pair starting at stage (ls & ~1) + 4, possibly the next unit's).
+    struct TgtA {
+        uint32_t a;
+        int vb;
+    };
+    auto target_a = [&](int ls) __attribute__((always_inline)) {
+        const int xp = (ls & ~1) + 4;
+        const bool in_cur = xp < n_st4;
+        const int xl = in_cur ? xp : xp - n_st4;
+        const Orig& o = in_cur ? ocur : onxt;
+        const int kend = min((o.sbeg + o.nst) * 64, Kp);   // live K bytes end (o.nst = 0: none)
+        TgtA t;
+        t.vb = kend - (o.sbeg + xl) * 64;
+        t.a = t.vb > 0 ? o.a + (uint32_t)xl * 64u : kOOB;
+        return t;
     };
     // VMEM items issued at local stage ls (static slot u = ls & 3): DA
     // A-DMAs and FN B-loads for stage ls+3 and, on odd stages, the NSDW scale
     // DMAs of 256-K group (ls+3)/2 into buffer ((ls+3)/2) & 1.
-    auto issue_item = [&](auto U, auto D, const Tgt& t3) __attribute__((always_inline)) {
+    auto issue_item = [&](auto U, auto D, const Tgt& t3, const TgtA& ta)
+        __attribute__((always_inline)) {
         constexpr int u = decltype(U)::value;
         constexpr int d = decltype(D)::value;
         if constexpr (d < T::DA) {
-            a_dma(aslot(std::integral_constant<int, u + 3>{}), std::integral_constant<int, d>{}, t3);
+            a_dma(std::integral_constant<int, (u >> 1) + 2>{}, std::integral_constant<int, u & 1>{},
+                  std::integral_constant<int, d>{}, ta.a, ta.vb);
         } else if constexpr (d < T::DA + T::FN) {
             constexpr int j = d - T::DA;
             rb[(u + 3) & 3][j] = load16s(rB, voB[j] | t3.tv, t3.b);
@@ -598,22 +656,32 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     constexpr int EPI_OPS = SPLIT ? 0 : T::FM * (T::FN / 2) + FD;
     static_assert(NI_EVEN + EPI_OPS <= 63 && NI_ODD <= 63, "vmcnt is 6 bits");
 
-    // A fragment x of the stage in ring slot BUF -> register ra[R].
-    auto read_a = [&](auto BUF, auto X, auto R) __attribute__((always_inline)) {
-        ra[decltype(R)::value] = *reinterpret_cast<const i32x4*>(
-            aslot(BUF) + (wm * T::FM + decltype(X)::value) * 1024 + lane * 16);
+    // A fragment x of the wave, half H of pair K of the iteration -> ra[R].
+    auto read_a = [&](auto PK, auto H, auto X, auto R) __attribute__((always_inline)) {
+        constexpr int x = decltype(X)::value;
+        ra[decltype(R)::value] =
+            ds_read16<x * 2048>(lds_addr(qp(PK)) + loA[decltype(H)::value] + (uint32_t)(wm * T::FM * 2048));
     };
 
     // One scale dword of the group in buffer BUF -> register set SET
     // (k < SA: A dword k, else B dword k - SA).
     auto read_scale = [&](auto BUF, auto SET, auto KI) __attribute__((always_inline)) {
-        constexpr int set = decltype(SET)::value, k = decltype(KI)::value;
-        if constexpr (k < T::SA)
-            sa[set][k] = *reinterpret_cast<const int*>(
-                sbuf(BUF) + (((wm * T::WM) >> 5) + k) * 256 + lane * 4);
-        else
-            sb[set][k - T::SA] = *reinterpret_cast<const int*>(
-                sbuf(BUF) + T::NSDA * 1024 + (((wn * T::WN) >> 5) + k - T::SA) * 256 + lane * 4);
+        constexpr int set = decltype(SET)::value, k = decltype(KI)::value, b = decltype(BUF)::value & 1;
+        if constexpr (k < T::SA) sa[set][k] = ds_read4<k * 256>(scA[b]);
+        else sb[set][k - T::SA] = ds_read4<(k - T::SA) * 256>(scB[b]);
+    };
+    static_assert(T::FM >= 4, "the A look-ahead and scale-read schedule needs 4+ fragments");
+    // Gap of scale read k of an odd stage: spread over [FN, (FM-2)*FN), so
+    // every scale read is older than the two look-ahead fragment reads that
+    // end the stage (which makes the wait of the next stage's first MFMA
+    // cover them).
+    constexpr int NSR = T::SA + T::SB;
+    constexpr auto scale_gap = [](int k) constexpr { return T::FN + (k * ((T::FM - 3) * T::FN)) / NSR; };
+    // Scale reads of an odd stage at gaps in [g0, g1).
+    constexpr auto scales_in = [scale_gap](int g0, int g1) constexpr {
+        int n = 0;
+        for (int k = 0; k < NSR; ++k) n += (scale_gap(k) >= g0 && scale_gap(k) < g1) ? 1 : 0;
+        return n;
     };
 
     // Load targets of the stage three ahead.  GEN kernels (dead stages or a
@@ -621,6 +689,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     // them in `run` and advance it by constant steps, switching to the next
     // unit's origin when the load stage crosses the unit end.
     Tgt run{};
+    TgtA runA{};
 
     // A stage issues its FM x FN MFMAs one by one; the gap after MFMA g gets
     // at most a few other instructions, spread so that with one wave per
@@ -639,7 +708,6 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         constexpr int NI = ((u & 1) == 0) ? NI_EVEN : NI_ODD;   // issues of this stage
         constexpr int NIP = ((u & 1) == 0) ? NI_ODD : NI_EVEN;  // issues of the previous one
         constexpr int NG = T::FM * T::FN;                       // MFMAs (= gaps) per stage
-        constexpr int NS = T::SA + T::SB;                       // scale dwords per group
         // Everything issued two or more stages ago has landed (A of ls+1 for
         // this stage's look-ahead reads, B and scales of ls); the previous
         // stage's issues may still be in flight.
@@ -658,22 +726,33 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         }
         __builtin_amdgcn_sched_barrier(0);
         Tgt t3;
+        TgtA ta;
         if constexpr (GEN) {
             t3 = target(ls + 3);
+            ta = target_a(ls);
         } else {
-            if constexpr (u == 1) {  // the only stage whose load stage can be a unit's first
+            if constexpr (u == 1) {  // the only stage whose B stage can be a unit's first
                 const bool sw = ls + 3 == n_st4;
-                run.a = sw ? onxt.a : run.a;
                 run.b = sw ? onxt.b : run.b;
                 run.as = sw ? onxt.as : run.as;
                 run.bs = sw ? onxt.bs : run.bs;
             }
+            if constexpr (u == 0) {  // the only stage whose A pair can be a unit's first
+                runA.a = ls + 4 == n_st4 ? onxt.a : runA.a;
+            }
             t3 = run;
+            ta = runA;
         }
         int sav[T::SA], sbv[T::SB];
         static_for<T::SA>([&](auto i) { sav[i] = sa[sset][i]; });
         static_for<T::SB>([&](auto j) { sbv[j] = sb[sset][j]; });
         if constexpr (GEN) {
+            // The selects read the scale registers: wait for their ds_reads
+            // first (only fragment 1's read, the youngest, may stay pending).
+            constexpr int ar0 = (T::FM * u) & 3;
+            wait_lgkm_for<1>(ra[ar0]);
+            static_for<T::SA>([&](auto i) { tie_after(sav[i]); });
+            static_for<T::SB>([&](auto i) { tie_after(sbv[i]); });
             const bool tail = ktail && ls < cur.nst && cur.sbeg + ls == S_total - 1 && hi_lane;
             static_for<T::SA>([&](auto i) { sav[i] = tail ? 0x7F7F7F7F : sav[i]; });
             static_for<T::SB>([&](auto j) { sbv[j] = tail ? 0x7F7F7F7F : sbv[j]; });
@@ -682,6 +761,21 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             constexpr int g = decltype(G_)::value;
             constexpr int c = g / T::FN, j = g % T::FN;
             constexpr int ar = (T::FM * u + c) & 3;
+            using PKu = std::integral_constant<int, (u >> 1)>;        // pair of this stage
+            using PKn = std::integral_constant<int, ((u + 1) >> 1)>;  // pair of the next
+            if constexpr (j == 0) {
+                // Fragment c was read at gap (c-2)*FN (of the previous stage
+                // for c < 2).  Younger LDS reads: the next fragment read, and
+                // (odd stages) the scale reads since that gap.  At c = 0 this
+                // also covers the scales the stage uses (read earlier).
+                constexpr int nyoung =
+                    1 + ((u & 1) && c >= 2 ? scales_in((c - 2) * T::FN, c * T::FN) : 0);
+                wait_lgkm_for<nyoung>(ra[ar]);
+                if constexpr (c == 0) {
+                    static_for<T::SA>([&](auto i) { tie_after(sav[i]); });
+                    static_for<T::SB>([&](auto i) { tie_after(sbv[i]); });
+                }
+            }
             constexpr int opb = (j & 1) + 2 * h;
             constexpr int opa = (c & 1) + 2 * h;
             // K-tail stages select scales with VALU ops: keep the wait states there.
@@ -694,10 +788,11 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                 // look-ahead A read: fragment c+2 of this stage or of the next
                 constexpr int xn = c + 2;
                 if constexpr (xn < T::FM)
-                    read_a(std::integral_constant<int, u>{}, std::integral_constant<int, xn>{},
+                    read_a(PKu{}, std::integral_constant<int, u & 1>{},
+                           std::integral_constant<int, xn>{},
                            std::integral_constant<int, (T::FM * u + xn) & 3>{});
                 else
-                    read_a(std::integral_constant<int, u + 1>{},
+                    read_a(PKn{}, std::integral_constant<int, (u + 1) & 1>{},
                            std::integral_constant<int, xn - T::FM>{},
                            std::integral_constant<int, (T::FM * u + xn) & 3>{});
             }
@@ -706,16 +801,13 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                 constexpr int d = decltype(D)::value;
                 constexpr int span = NG - 2 * T::FN > 0 ? NG - 2 * T::FN : 1;
                 constexpr int gi = T::FN + T::FN / 2 + d * span / NI;
-                if constexpr ((gi < NG ? gi : NG - 1) == g) issue_item(U, D, t3);
+                if constexpr ((gi < NG ? gi : NG - 1) == g) issue_item(U, D, t3, ta);
             });
             // Odd stages: the next group's scale dwords (DMA'd two stages
-            // ago) over the middle half of the stage.
+            // ago), after this gap's fragment read.
             if constexpr ((u & 1) == 1) {
-                static_for<NS>([&](auto KI) {
-                    constexpr int k = decltype(KI)::value;
-                    constexpr int step = (NG / 2) / NS > 0 ? (NG / 2) / NS : 1;
-                    constexpr int gs = NG / 4 + 1 + k * step;
-                    if constexpr ((gs < NG ? gs : NG - 1) == g)
+                static_for<NSR>([&](auto KI) {
+                    if constexpr (scale_gap(decltype(KI)::value) == g)
                         read_scale(std::integral_constant<int, ((u + 1) >> 1) & 1>{},
                                    std::integral_constant<int, ((u + 1) >> 1) & 1>{}, KI);
                 });
@@ -723,11 +815,12 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             __builtin_amdgcn_sched_barrier(0);
         });
         if constexpr (!GEN) {  // advance the running targets to stage ls+4
-            run.a += 64u;
             run.b += 1024u;
             if constexpr ((u & 1) == 0) {  // load stage ls+3 was odd: next 256-K group
                 run.as += 256u;
                 run.bs += 256u;
+            } else {                       // both halves of the A pair issued
+                runA.a += 128u;
             }
         }
     };
@@ -764,30 +857,45 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     }
     factor_dma(cur, 0);
 
-    // ---- prologue: scale groups 0 and 1, then stages 0..2 (A, B) of the first unit
+    // ---- prologue: scale groups 0 and 1, A pair 0, B stage 0, A pair 1,
+    // B stages 1 and 2 of the first unit (pair p is what local stage 2p-4
+    // would DMA: target_a(2p - 4)).
     static_for<2>([&](auto P) {
         const Tgt t = target(2 * decltype(P)::value);
         static_for<T::NSDW>([&](auto i) { scale_dma(P, i, t); });
     });
-    static_for<3>([&](auto P) {
-        constexpr int ps = decltype(P)::value;
-        const Tgt t = target(ps);
-        static_for<T::DA>([&](auto d) {
-            a_dma(aslot(P), d, t);
+    auto b_stage = [&](auto S) __attribute__((always_inline)) {
+        constexpr int ps = decltype(S)::value;
+        const Tgt tb = target(ps);
+        static_for<T::FN>([&](auto j) { rb[ps][j] = load16s(rB, voB[j] | tb.tv, tb.b); });
+    };
+    auto a_pair = [&](auto P) __attribute__((always_inline)) {
+        const TgtA t = target_a(2 * decltype(P)::value - 4);
+        static_for<2>([&](auto H) {
+            static_for<T::DA>([&](auto d) { a_dma(P, H, d, t.a, t.vb); });
         });
-        static_for<T::FN>([&](auto j) { rb[ps][j] = load16s(rB, voB[j] | t.tv, t.b); });
-    });
+    };
+    a_pair(std::integral_constant<int, 0>{});
+    b_stage(std::integral_constant<int, 0>{});
+    a_pair(std::integral_constant<int, 1>{});
+    b_stage(std::integral_constant<int, 1>{});
+    b_stage(std::integral_constant<int, 2>{});
     // The first stage is entered as if stages "-2" and "-1" had run: wait
-    // for everything but stage 2's issues, then read the scales of group 0
-    // and A fragments 0 and 1.
-    wait_vmcnt<T::DA + T::FN>();
+    // for everything but A pair 1 and B stages 1 and 2, then read the scales
+    // of group 0 and A fragments 0 and 1.
+    wait_vmcnt<2 * T::DA + 2 * T::FN>();
     barrier();
-    read_scales(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    static_for<NSR>([&](auto KI) {
+        read_scale(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, KI);
+    });
     read_a(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{},
-           std::integral_constant<int, 0>{});
-    read_a(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{},
-           std::integral_constant<int, 1>{});
-    if constexpr (!GEN) run = target(3);
+           std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    read_a(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{},
+           std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+    if constexpr (!GEN) {
+        run = target(3);
+        runA = target_a(0);
+    }
 
     const int row_l = wm * T::WM + (lane & 15);
     const int q = lane >> 4;
@@ -798,6 +906,12 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     using I3 = std::integral_constant<int, 3>;
     using FT = std::integral_constant<bool, true>;
     using FF = std::integral_constant<bool, false>;
+    auto rotate = [&]() __attribute__((always_inline)) {
+        uint8_t* t = q2;
+        q2 = q1;
+        q1 = q0;
+        q0 = t;
+    };
     for (int id = blockIdx.x; id < units; id += G) {
         {   // first iteration, peeled: its stage 0 starts the accumulators
             const bool post = id != (int)blockIdx.x;
@@ -810,12 +924,14 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             stage(I1{}, FF{}, 1, post);
             stage(I2{}, FF{}, 2, false);
             stage(I3{}, FF{}, 3, false);
+            rotate();
         }
         for (int ls0 = 4; ls0 < n_st4; ls0 += 4) {
             stage(I0{}, FF{}, ls0, false);
             stage(I1{}, FF{}, ls0 + 1, false);
             stage(I2{}, FF{}, ls0 + 2, false);
             stage(I3{}, FF{}, ls0 + 3, false);
+            rotate();
         }
         // The next unit's first stage would wait and sync here; doing it now
         // also makes this unit's factor bytes (and the table) visible.

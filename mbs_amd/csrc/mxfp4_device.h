@@ -127,6 +127,47 @@ __device__ __forceinline__ void wait_lgkmcnt0()
     __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (3 << 14));
 }
 
+// LDS reads written as instructions, for loops that schedule and wait for
+// their LDS traffic themselves (s_waitcnt lgkmcnt counted by the caller):
+// the compiler does not see them as memory accesses, so it neither waits
+// for them nor makes them wait for LDS DMA it cannot prove disjoint.
+// `addr` is an LDS byte address, OFF a compile-time offset (< 65536).
+template <int OFF>
+__device__ __forceinline__ i32x4 ds_read16(uint32_t addr)
+{
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset range");
+    i32x4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ int ds_read4(uint32_t addr)
+{
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset range");
+    int v;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
+    return v;
+}
+// s_waitcnt lgkmcnt(N) that also "rewrites" `reg`, so every later use of
+// reg (an MFMA operand) is ordered after the wait.
+template <int N, class R>
+__device__ __forceinline__ void wait_lgkm_for(R& reg)
+{
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(reg) : "n"(N));
+}
+// Orders later uses of `reg` after the preceding volatile asm (no code).
+template <class R>
+__device__ __forceinline__ void tie_after(R& reg)
+{
+    asm volatile("" : "+v"(reg));
+}
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void* p)
+{
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 // Workgroup barrier with no implied memory fence (the fence of
 // __syncthreads would force vmcnt(0) and drain the LDS DMA prefetch).  The
 // "memory" clobber keeps the compiler from moving LDS accesses across it;
