@@ -763,26 +763,27 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             constexpr int ar = (T::FM * u + c) & 3;
             using PKu = std::integral_constant<int, (u >> 1)>;        // pair of this stage
             using PKn = std::integral_constant<int, ((u + 1) >> 1)>;  // pair of the next
-            if constexpr (j == 0) {
-                // Fragment c was read at gap (c-2)*FN (of the previous stage
-                // for c < 2).  Younger LDS reads: the next fragment read, and
-                // (odd stages) the scale reads since that gap.  At c = 0 this
-                // also covers the scales the stage uses (read earlier).
-                constexpr int nyoung =
-                    1 + ((u & 1) && c >= 2 ? scales_in((c - 2) * T::FN, c * T::FN) : 0);
-                wait_lgkm_for<nyoung>(ra[ar]);
-                if constexpr (c == 0) {
-                    static_for<T::SA>([&](auto i) { tie_after(sav[i]); });
-                    static_for<T::SB>([&](auto i) { tie_after(sbv[i]); });
-                }
-            }
+            // Fragment c was read at gap (c-2)*FN (of the previous stage for
+            // c < 2).  LDS reads younger than it: the next fragment read and
+            // (odd stages) the scale reads since that gap; the first MFMA of
+            // the chunk waits for the rest.  At c = 0 that also covers the
+            // scales the stage uses (read before the look-ahead reads).
+            constexpr int nyoung =
+                1 + ((u & 1) && c >= 2 ? scales_in((c - 2) * T::FN, c * T::FN) : 0);
             constexpr int opb = (j & 1) + 2 * h;
             constexpr int opa = (c & 1) + 2 * h;
             // K-tail stages select scales with VALU ops: keep the wait states there.
-            if constexpr (first && !GEN)
-                mfma_fp4_first<opb, opa>(acc[c][j], rb[u][j], ra[ar], sbv[j / 2], sav[c / 2]);
-            else
-                mfma_fp4<opb, opa, GEN>(acc[c][j], rb[u][j], ra[ar], sbv[j / 2], sav[c / 2]);
+            if constexpr (j == 0) {
+                if constexpr (first && !GEN)
+                    mfma_fp4_first_w<opb, opa, nyoung>(acc[c][j], rb[u][j], ra[ar], sbv[j / 2], sav[c / 2]);
+                else
+                    mfma_fp4_w<opb, opa, nyoung, GEN>(acc[c][j], rb[u][j], ra[ar], sbv[j / 2], sav[c / 2]);
+            } else {
+                if constexpr (first && !GEN)
+                    mfma_fp4_first<opb, opa>(acc[c][j], rb[u][j], ra[ar], sbv[j / 2], sav[c / 2]);
+                else
+                    mfma_fp4<opb, opa, GEN>(acc[c][j], rb[u][j], ra[ar], sbv[j / 2], sav[c / 2]);
+            }
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (j == 0) {
                 // look-ahead A read: fragment c+2 of this stage or of the next

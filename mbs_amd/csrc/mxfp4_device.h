@@ -228,6 +228,44 @@ __device__ __forceinline__ void mfma_fp4(f32x4& acc, i32x4 a, i32x4 b, int sa, i
     }
 }
 
+// The same MFMAs preceded, in the same asm statement, by s_waitcnt
+// lgkmcnt(W): for operands read from LDS with explicit ds_read instructions,
+// whose completion the caller counts.  Keeping the wait inside the statement
+// orders it before the MFMA without a fake register definition (which would
+// make the compiler add wait states of its own); `volatile` keeps the
+// statement in order with the ds_read statements it counts.
+template <int OPA, int OPB, int W>
+__device__ __forceinline__ void mfma_fp4_first_w(f32x4& acc, i32x4 a, i32x4 b, int sa, int sb)
+{
+    static_assert(W >= 0 && W < 16, "lgkmcnt range");
+    asm volatile("s_waitcnt lgkmcnt(%9)\n\t"
+        "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, 0, %3, %4 op_sel:[%5,%6,0] "
+        "op_sel_hi:[%7,%8,0] cbsz:4 blgp:4"
+        : "=a"(acc)
+        : "v"(a), "v"(b), "v"(sa), "v"(sb), "n"(OPA & 1), "n"(OPB & 1), "n"(OPA >> 1),
+          "n"(OPB >> 1), "n"(W));
+}
+template <int OPA, int OPB, int W, bool NOP>
+__device__ __forceinline__ void mfma_fp4_w(f32x4& acc, i32x4 a, i32x4 b, int sa, int sb)
+{
+    static_assert(W >= 0 && W < 16, "lgkmcnt range");
+    if constexpr (NOP) {
+        asm volatile("s_waitcnt lgkmcnt(%9)\n\ts_nop 1\n\t"
+            "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[%5,%6,0] "
+            "op_sel_hi:[%7,%8,0] cbsz:4 blgp:4"
+            : "+a"(acc)
+            : "v"(a), "v"(b), "v"(sa), "v"(sb), "n"(OPA & 1), "n"(OPB & 1), "n"(OPA >> 1),
+              "n"(OPB >> 1), "n"(W));
+    } else {
+        asm volatile("s_waitcnt lgkmcnt(%9)\n\t"
+            "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[%5,%6,0] "
+            "op_sel_hi:[%7,%8,0] cbsz:4 blgp:4"
+            : "+a"(acc)
+            : "v"(a), "v"(b), "v"(sa), "v"(sb), "n"(OPA & 1), "n"(OPB & 1), "n"(OPA >> 1),
+              "n"(OPB >> 1), "n"(W));
+    }
+}
+
 // Wait states between the last MFMA writing an accumulator and any other
 // instruction reading it (gfx9 requires up to ~19 for a 16-pass XDL op).
 __device__ __forceinline__ void mfma_drain()
