@@ -366,7 +366,7 @@ struct BdShape {
     static constexpr int FBW = 256 * (1 + NBC);
     static_assert(BM <= 256, "one 256-byte chunk of A factor bytes");
     static_assert(NW == 1 ? NBC == 1 : NW >= 1 + NBC, "one factor DMA per wave");
-    static_assert(BM % 32 == 0, "pair halves of whole 16-row groups (swizzle parity)");
+    static_assert(BM % 16 == 0, "pair halves of whole 8-row DMA groups");
     static_assert(3 * PSLOT + 2 * SBUF <= 150 * 1024, "LDS budget");
 };
 
@@ -380,9 +380,10 @@ struct Unit {
 };
 
 // Chunk swizzle of an A pair slot: row r keeps its global 16-byte chunk c at
-// physical chunk c ^ swz(r).  Any 8 consecutive rows (and, per row parity,
-// any 16) then spread a fragment read (16 rows, one chunk) over all banks.
-__device__ __forceinline__ int a_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+// physical chunk c ^ (r & 7).  A fragment read (16 rows, one chunk per row)
+// then has no LDS bank conflicts on gfx950 (measured with SQ_LDS_BANK_CONFLICT:
+// unswizzled 128-byte rows conflict 4-way, this pattern not at all).
+__device__ __forceinline__ int a_swz(int r) { return r & 7; }
 
 // Persistent B-direct kernel: gridDim.x workgroups (at most one resident
 // set per CU) walk work units id = blockIdx.x + i*gridDim.x.  Per unit the
@@ -478,13 +479,13 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
 
     // Per-lane offsets within a tile, fixed for the whole kernel.
     // A DMA j of a pair half: lane i -> row 8j + i/8 of the half, physical
-    // chunk i%8, which holds global chunk (i%8) ^ swz(row); swz(row) =
-    // (i/8) ^ (j & 1) since the half starts at a multiple of 16 rows.
+    // chunk i%8, which holds global chunk (i%8) ^ swz(row); swz(row) = i/8
+    // since the half starts at a multiple of 8 rows.
     // cA: the lane's K-byte offset in the pair (K-tail and dead-stage masks).
     uint32_t voA[T::DA], cA[T::DA];
     static_for<T::DA>([&](auto d) {
         const int j = w * T::DA + d;
-        const int c = (lane & 7) ^ (lane >> 3) ^ (j & 1);
+        const int c = (lane & 7) ^ (lane >> 3);
         cA[d] = (uint32_t)(c * 16);
         voA[d] = (uint32_t)((8 * j + (lane >> 3)) * Kp + c * 16);
     });
