@@ -100,27 +100,27 @@ struct Config {
 };
 
 const Config kConfigs[] = {
-    {"tiled_256x256_w2x2", kTiled, 256, 256, 256, 1, {0.703f, 0.703f, 3.99f}, launch_tiled<T256x256>},
-    {"tiled_256x128_w2x2", kTiled, 256, 128, 256, 1, {0.502f, 0.502f, 1.26f}, launch_tiled<T256x128>},
-    {"tiled_128x256_w2x2", kTiled, 128, 256, 256, 1, {0.418f, 0.418f, 1.43f}, launch_tiled<T128x256>},
-    {"tiled_128x128_w2x2", kTiled, 128, 128, 256, 2, {0.282f, 0.503f, 0.58f}, launch_tiled<T128x128>},
-    {"tiled_64x256_w1x4", kTiled, 64, 256, 256, 2, {0.269f, 0.533f, 0.74f}, launch_tiled<T64x256>},
-    {"tiled_64x128_w1x2", kTiled, 64, 128, 128, 3, {0.232f, 0.427f, 0.25f}, launch_tiled<T64x128>},
-    {"tiled_64x64_w1x1", kTiled, 64, 64, 64, 4, {0.237f, 0.444f, 0.17f}, launch_tiled<T64x64>},
-    {"bdirect_256x256_w2x2", kTiled, 256, 256, 256, 1, {0.686f, 0.686f, 2.81f}, launch_bdirect<B256x256>, true},
-    {"bdirect_256x128_w2x2", kTiled, 256, 128, 256, 1, {0.521f, 0.521f, 0.77f}, launch_bdirect<B256x128>, true},
-    {"bdirect_128x256_w2x2", kTiled, 128, 256, 256, 1, {0.447f, 0.447f, 0.94f}, launch_bdirect<B128x256>, true},
-    {"bdirect_128x128_w2x2", kTiled, 128, 128, 256, 2, {0.338f, 0.536f, 0.47f}, launch_bdirect<B128x128>, true},
-    {"bdirect_64x256_w1x4", kTiled, 64, 256, 256, 2, {0.290f, 0.430f, 0.36f}, launch_bdirect<B64x256>, true},
-    {"bdirect_64x128_w1x2", kTiled, 64, 128, 128, 3, {0.243f, 0.395f, 0.15f}, launch_bdirect<B64x128>, true},
-    {"bdirect_64x64_w1x1", kTiled, 64, 64, 64, 4, {0.264f, 0.411f, 0.09f}, launch_bdirect<B64x64>, true},
-    {"bdirect_256x256_w1x4", kTiled, 256, 256, 256, 1, {0.650f, 0.650f, 2.66f}, launch_bdirect<B256x256w14>, true},
-    {"bdirect_256x128_w1x4", kTiled, 256, 128, 256, 1, {0.474f, 0.474f, 0.74f}, launch_bdirect<B256x128w14>, true},
-    {"bdirect_128x256_w1x4", kTiled, 128, 256, 256, 1, {0.394f, 0.394f, 0.92f}, launch_bdirect<B128x256w14>, true},
-    {"bdirect_192x256_w1x4", kTiled, 192, 256, 256, 1, {0.504f, 0.504f, 1.78f}, launch_bdirect<B192x256w14>, true},
-    {"bdirect_96x256_w1x4", kTiled, 96, 256, 256, 1, {0.351f, 0.351f, 0.37f}, launch_bdirect<B96x256w14>, true},
-    {"bdirect_64x512_w1x4", kTiled, 64, 512, 256, 1, {0.419f, 0.419f, 0.71f}, launch_bdirect<B64x512w14>, true},
-    {"bdirect_128x384_w1x4", kTiled, 128, 384, 256, 1, {0.508f, 0.508f, 1.54f}, launch_bdirect<B128x384w14>, true},
+    {"tiled_256x256_w2x2", kTiled, 256, 256, 256, 1, {0.851f, 0.851f, 9.13f}, launch_tiled<T256x256>},
+    {"tiled_256x128_w2x2", kTiled, 256, 128, 256, 1, {0.572f, 0.572f, 3.72f}, launch_tiled<T256x128>},
+    {"tiled_128x256_w2x2", kTiled, 128, 256, 256, 1, {0.536f, 0.536f, 2.32f}, launch_tiled<T128x256>},
+    {"tiled_128x128_w2x2", kTiled, 128, 128, 256, 2, {0.283f, 0.566f, 3.53f}, launch_tiled<T128x128>},
+    {"tiled_64x256_w1x4", kTiled, 64, 256, 256, 2, {0.295f, 0.591f, 2.90f}, launch_tiled<T64x256>},
+    {"tiled_64x128_w1x2", kTiled, 64, 128, 128, 3, {0.209f, 0.530f, 3.58f}, launch_tiled<T64x128>},
+    {"tiled_64x64_w1x1", kTiled, 64, 64, 64, 4, {0.228f, 0.228f, 3.30f}, launch_tiled<T64x64>},
+    {"bdirect_256x256_w2x2", kTiled, 256, 256, 256, 1, {0.612f, 0.612f, 6.57f}, launch_bdirect<B256x256>, true},
+    {"bdirect_256x128_w2x2", kTiled, 256, 128, 256, 1, {0.389f, 0.389f, 3.09f}, launch_bdirect<B256x128>, true},
+    {"bdirect_128x256_w2x2", kTiled, 128, 256, 256, 1, {0.415f, 0.415f, 3.38f}, launch_bdirect<B128x256>, true},
+    {"bdirect_128x128_w2x2", kTiled, 128, 128, 256, 2, {0.235f, 0.446f, 2.54f}, launch_bdirect<B128x128>, true},
+    {"bdirect_64x256_w1x4", kTiled, 64, 256, 256, 2, {0.235f, 0.434f, 2.40f}, launch_bdirect<B64x256>, true},
+    {"bdirect_64x128_w1x2", kTiled, 64, 128, 128, 3, {0.191f, 0.357f, 1.96f}, launch_bdirect<B64x128>, true},
+    {"bdirect_64x64_w1x1", kTiled, 64, 64, 64, 4, {0.198f, 0.274f, 1.59f}, launch_bdirect<B64x64>, true},
+    {"bdirect_256x256_w1x4", kTiled, 256, 256, 256, 1, {0.611f, 0.611f, 7.01f}, launch_bdirect<B256x256w14>, true},
+    {"bdirect_256x128_w1x4", kTiled, 256, 128, 256, 1, {0.383f, 0.383f, 3.03f}, launch_bdirect<B256x128w14>, true},
+    {"bdirect_128x256_w1x4", kTiled, 128, 256, 256, 1, {0.367f, 0.367f, 3.14f}, launch_bdirect<B128x256w14>, true},
+    {"bdirect_192x256_w1x4", kTiled, 192, 256, 256, 1, {0.467f, 0.467f, 4.17f}, launch_bdirect<B192x256w14>, true},
+    {"bdirect_96x256_w1x4", kTiled, 96, 256, 256, 1, {0.333f, 0.333f, 2.77f}, launch_bdirect<B96x256w14>, true},
+    {"bdirect_64x512_w1x4", kTiled, 64, 512, 256, 1, {0.428f, 0.428f, 3.26f}, launch_bdirect<B64x512w14>, true},
+    {"bdirect_128x384_w1x4", kTiled, 128, 384, 256, 1, {0.455f, 0.455f, 4.55f}, launch_bdirect<B128x384w14>, true},
     // skinny: bm = rows covered (16*MT), bn = B rows per workgroup (16*NF)
     // eff = streaming efficiency relative to the best variant (cold N=K=8192 timings)
     {"skinny_m16_n32_w16", kSkinny, 16, 32, 1024, 1, {0.95f, 0.f, 0.f}, launch_skinny<1, 2, 16, 4>},
@@ -207,7 +207,7 @@ bool make_plan(int config, int want_splits, int M, int N, int K, Plan* out)
 // stage time grows from cost.a (one workgroup per CU) to cost.b (wgs_per_cu
 // of them); split-K adds the fp32 partial round trip (the reduce kernel).
 // The constants were fitted to measured times (log-error least squares).
-constexpr double kLaunchNs = 4690.0;
+constexpr double kLaunchNs = 2000.0;
 constexpr double kSplitBytesPerNs = 2084.0;
 constexpr double kHbmBytesPerNs = 6000.0;
 // A fragments re-read from L2 by every skinny workgroup (measured ~25 TB/s
@@ -245,8 +245,58 @@ double plan_cost(const Plan& pl, int M, int N, int K)
            split_ns;
 }
 
+// Measured best plans (graph-replayed timings of every configuration and
+// split count on MI355X) for the shapes of the reference's published model
+// layers, the BASELINE configurations and a few squares.  Exact matches
+// take these; every other shape goes through the cost model.
+struct TunedPlan {
+    int M, N, K;
+    const char* config;
+    int splits;
+};
+const TunedPlan kTuned[] = {
+    {1024, 17408, 5120, "bdirect_192x256_w1x4", 1},  // 52.9 us
+    {1024, 1024, 5120, "bdirect_64x128_w1x2", 1},  // 10.7 us
+    {256, 7168, 2048, "bdirect_64x128_w1x2", 1},  // 7.1 us
+    {2048, 7168, 2048, "bdirect_256x256_w2x2", 1},  // 22.2 us
+    {256, 4096, 7168, "bdirect_64x128_w1x2", 1},  // 13.1 us
+    {2048, 4096, 7168, "bdirect_128x256_w1x4", 1},  // 30.3 us
+    {256, 2112, 7168, "bdirect_64x128_w1x2", 2},  // 13.1 us
+    {2048, 2112, 7168, "bdirect_96x256_w1x4", 1},  // 24.7 us
+    {1000, 1280, 512, "bdirect_64x128_w1x2", 1},  // 4.9 us
+    {3333, 5120, 512, "bdirect_64x128_w1x2", 1},  // 15.3 us
+    {1000, 5120, 12288, "bdirect_256x128_w1x4", 1},  // 40.1 us
+    {3333, 1280, 12288, "bdirect_128x256_w1x4", 1},  // 39.4 us
+    {8192, 10240, 5120, "bdirect_256x256_w2x2", 1},  // 186.5 us
+    {8192, 17408, 5120, "bdirect_192x256_w1x4", 1},  // 327.5 us
+    {8192, 5120, 17408, "bdirect_256x256_w2x2", 1},  // 295.7 us
+    {8192, 12288, 5120, "bdirect_128x384_w1x4", 1},  // 226.4 us
+    {8192, 8192, 8192, "bdirect_256x256_w2x2", 1},  // 219.7 us
+    {128, 256, 512, "bdirect_64x64_w1x1", 1},  // 4.5 us
+    {4096, 4096, 4096, "bdirect_256x256_w2x2", 1},  // 35.3 us
+    {512, 8192, 8192, "bdirect_64x256_w1x4", 1},  // 23.9 us
+    {64, 8192, 8192, "bdirect_64x64_w1x1", 4},  // 13.5 us
+    {2048, 2048, 2048, "bdirect_64x256_w1x4", 1},  // 9.4 us
+};
+
+int config_index(const char* name)
+{
+    for (int i = 0; i < kNumConfigs; ++i)
+        if (std::strcmp(kConfigs[i].name, name) == 0) return i;
+    return -1;
+}
+
 bool choose_plan(int M, int N, int K, size_t ws_avail, Plan* best)
 {
+    for (const TunedPlan& t : kTuned) {
+        if (t.M != M || t.N != N || t.K != K) continue;
+        const int c = config_index(t.config);
+        Plan pl;
+        if (c >= 0 && make_plan(c, t.splits, M, N, K, &pl) && pl.ws_bytes <= ws_avail) {
+            *best = pl;
+            return true;
+        }
+    }
     bool have = false;
     double best_cost = 0;
     for (int i = 0; i < kNumConfigs; ++i) {
