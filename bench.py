@@ -13,7 +13,8 @@ Also reported (same JSON line): the decode shapes of configs[2]
 (M in {1,4,16,32}, N=K=8192) measured cold -- ten rotating weight copies,
 more than the 256 MB MALL -- replayed from a HIP graph; and the CPU baseline
 (the oracle's restatement of the reference's run_torch on this host's cores,
-on a bounded sample).
+on a bounded sample); and the grouped (mixture-of-experts) GEMM on
+configs[3]'s expert shapes, one launch against one dense launch per expert.
 
 One GPU only: --gpus above 1 exits with an explanation.
 """
@@ -109,6 +110,61 @@ def decode_bench(dev, Ms=(1, 4, 16, 32), N=8192, K=8192, copies=10, replays=20):
     return res
 
 
+def grouped_bench(dev, experts=8, rows=256, shapes=((7168, 2048), (4096, 7168), (2112, 7168)),
+                  replays=10):
+    """Grouped GEMM over `experts` experts of `rows` tokens each (configs[3]'s
+    M=256 expert shapes, 8 experts = 2048 tokens): one grouped launch against
+    one dense launch per expert, both replayed from HIP graphs."""
+    import torch
+
+    import mbs_amd
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(1003)
+    M = experts * rows
+    offs = torch.arange(0, M + 1, rows, dtype=torch.int32, device=dev)
+    res = {}
+    for N, K in shapes:
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        w = (torch.randn(experts * N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        A, As = mbs_amd.quantize_mxfp4(x, shuffle=True)
+        Bp, Bs_all = [], []
+        for e in range(experts):
+            wq, ws = mbs_amd.quantize_mxfp4(w[e * N:(e + 1) * N], shuffle=True)
+            Bp.append(mbs_amd.shuffle_weight(wq))
+            Bs_all.append(ws.reshape(-1))
+        B, Bs = torch.stack(Bp), torch.stack(Bs_all)
+        snp = ((K + 31) // 32 + 7) // 8 * 8
+        grouped = lambda: mbs_amd.gemm_a4w4_grouped(A, B, As, Bs, offs)
+        dense = lambda: [mbs_amd.gemm_a4w4(A[e * rows:(e + 1) * rows], B[e],
+                                           As.reshape(-1)[e * rows * snp:(e + 1) * rows * snp], Bs[e])
+                         for e in range(experts)]
+        times = {}
+        for name, fn in (("grouped", grouped), ("per_expert", dense)):
+            fn()
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                fn()
+            gr.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(replays):
+                gr.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            times[name] = e0.elapsed_time(e1) * 1e3 / replays
+            del gr
+        flops = 2.0 * M * N * K
+        res[f"{experts}x{rows}x{N}x{K}"] = {
+            "grouped_us": round(times["grouped"], 2), "per_expert_us": round(times["per_expert"], 2),
+            "grouped_TFLOPS": round(flops / times["grouped"] / 1e6, 1),
+            "speedup_vs_per_expert": round(times["per_expert"] / times["grouped"], 3)}
+        del A, As, B, Bs, Bp, Bs_all, x, w
+    return res
+
+
 def cpu_baseline(x, w, rows=8192, reps=3):
     """The oracle's run_torch restatement (dequant to fp32, torch.mm fp32,
     bf16) on this host: `rows` rows of the config-1 A against the full W."""
@@ -142,6 +198,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-decode", action="store_true", help="skip the decode shapes")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-grouped", action="store_true", help="skip the grouped (MoE) shapes")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 20 device-to-device copies of MIB MiB (scales the HBM "
                          "FETCH_SIZE/WRITE_SIZE counters) and exit")
@@ -198,6 +255,8 @@ def main():
     if not args.no_decode:
         line["decode"] = decode_bench(dev)
     del A, B, As, Bs
+    if not args.no_grouped:
+        line["grouped"] = grouped_bench(dev)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(x, w)
     print(json.dumps(line), flush=True)

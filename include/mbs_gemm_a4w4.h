@@ -65,6 +65,29 @@ int mbs_gemm_a4w4_launch(const uint8_t* A, const uint8_t* B, const uint8_t* ASca
                          int scaleN_pad, void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* Grouped (mixture-of-experts) GEMM: E = num_groups experts share one launch.
+ * Expert e owns rows [group_offsets[e], group_offsets[e+1]) of A (and of out)
+ * and the e-th block of the stacked weights:
+ *   B       [E][N, K/2]  each block (16,16)-preshuffled as above,
+ *   BScale  [E][round_up(N,32) * scaleN_pad]  each block shuffled as above,
+ *   BFactor [E][N] (or NULL with AFactor NULL);
+ * A, AScale and AFactor cover all M rows as in mbs_gemm_a4w4_launch.
+ * group_offsets: device int32 [E+1], group_offsets[0] = 0, non-decreasing,
+ * every entry a multiple of 32 (pad each expert's token block, as MoE
+ * routing usually does), group_offsets[E] <= M; it is read by the kernel,
+ * not checked on the host.  Rows past group_offsets[E] are not written.
+ * config: -1 for the heuristic, else 0 <= config <
+ * mbs_gemm_a4w4_grouped_num_configs().  Each expert's rows give the same
+ * bytes as mbs_gemm_a4w4_launch on that expert alone.  No counterpart in the
+ * reference (its launcher takes one weight matrix). */
+int mbs_gemm_a4w4_grouped_launch(const uint8_t* A, const uint8_t* B, const uint8_t* AScale,
+                                 const uint8_t* BScale, const uint8_t* AFactor,
+                                 const uint8_t* BFactor, const int* group_offsets, int num_groups,
+                                 void* out, int M, int N, int K, int Mpad, int scaleN_pad,
+                                 int config, void* stream);
+int mbs_gemm_a4w4_grouped_num_configs(void);
+const char* mbs_gemm_a4w4_grouped_config_name(int config);
+
 /* Workspace the heuristic launch of (M,N,K) wants (0 if it needs none).
  * Passing less makes mbs_gemm_a4w4_launch fall back to a no-split plan.
  * No counterpart in the reference (its launcher never splits K). */

@@ -67,6 +67,20 @@ def gemm_a4w4(A, B, A_scale, B_scale, A_factor=None, B_factor=None):
     return ext().gemm_a4w4(A, B, A_scale, B_scale, A_factor, B_factor)
 
 
+def gemm_a4w4_grouped(A, B, A_scale, B_scale, group_offsets, A_factor=None, B_factor=None,
+                      config: int = -1):
+    """Grouped (mixture-of-experts) GEMM in one launch.
+
+    Expert e owns rows [group_offsets[e], group_offsets[e+1]) of A and of the
+    output, and the e-th [N, K/2] preshuffled block of B (B is [E, N, K/2] or
+    [E*N, K/2]), its shuffled scale block and its N factor bytes.  Offsets are
+    int32 [E+1]: 0 first, non-decreasing multiples of 32 (pad each expert's
+    token block), last <= M.  Each expert's rows equal ``gemm_a4w4`` of that
+    expert alone.  Rows past the last offset are not written."""
+    return ext().gemm_a4w4_grouped(A, B, A_scale, B_scale, group_offsets, A_factor, B_factor,
+                                   config)
+
+
 def quantize_mxfp4(x, shuffle: bool = True, pad_byte: int = 127):
     """bf16 [R,K] device tensor -> (packed u8 [R,K/2], E8M0 scales);
     shuffled [round_up(R,32), scaleN_pad] when ``shuffle`` else plain [R,K/32]."""

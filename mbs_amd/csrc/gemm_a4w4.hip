@@ -42,6 +42,7 @@ MBS_BDIRECT_SHAPES_B(MBS_BDIRECT_EXTERN)
 MBS_BDIRECT_SHAPES_C(MBS_BDIRECT_EXTERN)
 MBS_BDIRECT_SHAPES_D(MBS_BDIRECT_EXTERN)
 MBS_SKINNY_SHAPES(MBS_SKINNY_EXTERN)
+MBS_GROUPED_SHAPES(MBS_GROUPED_EXTERN)
 
 // ======================================================================
 // Split-K reduction: out[m][n..n+3] = epilogue(sum_s ws[s][m][n..n+3])
@@ -383,6 +384,72 @@ int run_plan(const Plan& pl, const uint8_t* A, const uint8_t* B, const uint8_t* 
     return MBS_OK;
 }
 
+// ------------------------------------------------------------ grouped GEMM
+// Persistent configurations with a grouped (MoE) variant; `dense` names the
+// dense configuration whose cost constants rank them.
+struct GroupedConfig {
+    const char* dense;
+    hipError_t (*launch)(const GemmArgs&, dim3, bool, bool, hipStream_t);
+};
+const GroupedConfig kGrouped[] = {
+    {"bdirect_256x256_w2x2", launch_bdirect_grouped<B256x256>},
+    {"bdirect_128x256_w1x4", launch_bdirect_grouped<B128x256w14>},
+    {"bdirect_64x256_w1x4", launch_bdirect_grouped<B64x256>},
+    {"bdirect_64x128_w1x2", launch_bdirect_grouped<B64x128>},
+};
+constexpr int kNumGrouped = (int)(sizeof(kGrouped) / sizeof(kGrouped[0]));
+
+// Upper bound of the grouped tile count: every expert adds at most one
+// partial M-tile to the ceil(M / BM) full ones.
+int grouped_units_bound(const Config& c, int M, int N, int E)
+{
+    return ((M + c.bm - 1) / c.bm + E) * ((N + c.bn - 1) / c.bn);
+}
+
+// Config choice: the dense cost model at the tile count the experts' padded
+// row blocks give on average (half a tile of padding per expert).
+int choose_grouped(int M, int N, int K, int E)
+{
+    int best = 0;
+    double best_cost = 0;
+    for (int g = 0; g < kNumGrouped; ++g) {
+        const int c = config_index(kGrouped[g].dense);
+        const int Meff = M + E * kConfigs[c].bm / 2;
+        Plan pl;
+        if (!make_plan(c, 1, Meff, N, K, &pl)) continue;
+        const double cst = plan_cost(pl, Meff, N, K);
+        if (g == 0 || cst < best_cost) {
+            best = g;
+            best_cost = cst;
+        }
+    }
+    return best;
+}
+
+int run_grouped(int g, const uint8_t* A, const uint8_t* B, const uint8_t* As, const uint8_t* Bs,
+                const uint8_t* Af, const uint8_t* Bf, const int* groups, int E, void* out, int M,
+                int N, int K, int snp, void* stream)
+{
+    const Config& c = kConfigs[config_index(kGrouped[g].dense)];
+    GemmArgs a{};
+    a.A = A; a.B = B; a.As = As; a.Bs = Bs; a.Af = Af; a.Bf = Bf;
+    a.out = static_cast<uint16_t*>(out);
+    a.M = M; a.N = N; a.K = K; a.snp = snp;
+    a.tiles_m = 0;  // computed on the device from the expert offsets
+    a.tiles_n = (N + c.bn - 1) / c.bn;
+    split_stages(K, 1, &a.sps, &a.splits);
+    a.groups = groups;
+    a.n_groups = E;
+    const int S_total = stages_of(K);
+    const bool gen = (K % 128) != 0 || a.sps % 4 != 0 || S_total % a.sps != 0;
+    const int units = grouped_units_bound(c, M, N, E);
+    const dim3 grid((unsigned)std::min(units, kNumCUs * c.wgs_per_cu));
+    (void)hipGetLastError();
+    const hipError_t e = kGrouped[g].launch(a, grid, gen, false, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(MBS_ERR_LAUNCH, std::string("launch failed: ") + hipGetErrorString(e));
+    return MBS_OK;
+}
+
 }  // namespace
 }  // namespace mbs
 
@@ -425,6 +492,36 @@ int mbs_gemm_a4w4_launch(const uint8_t* A, const uint8_t* B, const uint8_t* ASca
         return fail(MBS_ERR_CONFIG, "no kernel configuration fits this problem");
     return run_plan(pl, A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, scaleN_pad,
                     workspace, workspace_bytes, stream);
+}
+
+int mbs_gemm_a4w4_grouped_launch(const uint8_t* A, const uint8_t* B, const uint8_t* AScale,
+                                 const uint8_t* BScale, const uint8_t* AFactor,
+                                 const uint8_t* BFactor, const int* group_offsets, int num_groups,
+                                 void* out, int M, int N, int K, int Mpad, int scaleN_pad,
+                                 int config, void* stream)
+{
+    set_last_error("");
+    int st = validate(A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, Mpad, scaleN_pad);
+    if (st != MBS_OK) return st;
+    if (!group_offsets) return fail(MBS_ERR_ARGUMENT, "null group_offsets");
+    if (num_groups < 1 || num_groups > kMaxGroups)
+        return fail(MBS_ERR_ARGUMENT, "num_groups must be in [1, " + std::to_string(kMaxGroups) + "]");
+    const int64_t Npad = (N + 31) / 32 * 32;
+    if ((int64_t)num_groups * N * (K / 2) >= (1ll << 31) ||
+        (int64_t)num_groups * Npad * scaleN_pad >= (1ll << 31) || (int64_t)num_groups * N >= (1ll << 31))
+        return fail(MBS_ERR_ARGUMENT, "stacked expert weights too large for 32-bit buffer offsets");
+    if (config < -1 || config >= kNumGrouped)
+        return fail(MBS_ERR_CONFIG, "grouped config out of range");
+    const int g = config >= 0 ? config : choose_grouped(M, N, K, num_groups);
+    return run_grouped(g, A, B, AScale, BScale, AFactor, BFactor, group_offsets, num_groups, out, M,
+                       N, K, scaleN_pad, stream);
+}
+
+int mbs_gemm_a4w4_grouped_num_configs(void) { return kNumGrouped; }
+
+const char* mbs_gemm_a4w4_grouped_config_name(int config)
+{
+    return (config >= 0 && config < kNumGrouped) ? kGrouped[config].dense : "";
 }
 
 int mbs_gemm_a4w4_num_configs(void) { return kNumConfigs; }

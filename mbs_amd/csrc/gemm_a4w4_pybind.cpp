@@ -293,6 +293,65 @@ at::Tensor dequant_mxfp4(at::Tensor packed, at::Tensor scale_shuffled, bool b_pr
     return out;
 }
 
+// Grouped (MoE) GEMM: out[rows of expert e] = A[rows] @ B[e]^T (see
+// mbs_gemm_a4w4_grouped_launch).  B: [E, N, K/2] or [E*N, K/2] bytes,
+// B_scale: E shuffled blocks, group_offsets: int32 [E+1] (a host tensor is
+// checked -- 0 first, non-decreasing multiples of 32, last <= M -- and
+// copied to the device; a device tensor is used as it is).
+at::Tensor gemm_a4w4_grouped(at::Tensor A, at::Tensor B, at::Tensor A_scale, at::Tensor B_scale,
+                             at::Tensor group_offsets, c10::optional<at::Tensor> A_factor,
+                             c10::optional<at::Tensor> B_factor, int64_t config)
+{
+    TORCH_CHECK(group_offsets.dim() == 1 && group_offsets.numel() >= 2 &&
+                    group_offsets.scalar_type() == at::kInt,
+                "gemm_a4w4_grouped: group_offsets must be an int32 vector of E+1 entries");
+    const int64_t E = group_offsets.numel() - 1;
+    TORCH_CHECK(A.is_cuda() && B.is_cuda() && A.dim() == 2, "gemm_a4w4_grouped: A, B on device, A 2D");
+    TORCH_CHECK(B.element_size() == 1 && A.element_size() == 1, "gemm_a4w4_grouped: 1-byte A and B");
+    const int64_t M = A.size(0), Kp = A.size(1), K = Kp * 2;
+    TORCH_CHECK(B.numel() % (E * Kp) == 0, "gemm_a4w4_grouped: B must hold E blocks of [N, K/2]");
+    const int64_t N = B.numel() / (E * Kp);
+    TORCH_CHECK(B.size(-1) == Kp, "gemm_a4w4_grouped: B and A disagree on K");
+    const int64_t snp = scale_pad(K), Mpad = round_up(M, 32), Npad = round_up(N, 32);
+    TORCH_CHECK(A_scale.is_cuda() && B_scale.is_cuda(), "gemm_a4w4_grouped: scales must be on device");
+    TORCH_CHECK(A_scale.numel() >= Mpad * snp, "gemm_a4w4_grouped: A_scale too small");
+    TORCH_CHECK(B_scale.numel() >= E * Npad * snp, "gemm_a4w4_grouped: B_scale too small");
+    TORCH_CHECK(A_factor.has_value() == B_factor.has_value(),
+                "gemm_a4w4_grouped: A_factor and B_factor must be given together");
+    at::Tensor goff = group_offsets;
+    if (!goff.is_cuda()) {
+        auto g = goff.contiguous();
+        const int32_t* h = g.data_ptr<int32_t>();
+        TORCH_CHECK(h[0] == 0, "gemm_a4w4_grouped: group_offsets[0] must be 0");
+        for (int64_t e = 0; e < E; ++e)
+            TORCH_CHECK(h[e + 1] >= h[e] && h[e + 1] % 32 == 0,
+                        "gemm_a4w4_grouped: group_offsets must be non-decreasing multiples of 32");
+        TORCH_CHECK(h[E] <= M, "gemm_a4w4_grouped: group_offsets[E] exceeds the rows of A");
+        goff = g.to(A.device());
+    } else {
+        TORCH_CHECK(goff.device() == A.device(), "gemm_a4w4_grouped: group_offsets on another device");
+        goff = goff.contiguous();
+    }
+    c10::DeviceGuard guard(A.device());
+    auto Au = as_bytes(A), Bu = as_bytes(B), Asu = as_bytes(A_scale), Bsu = as_bytes(B_scale);
+    at::Tensor Af, Bf;
+    if (A_factor.has_value()) {
+        Af = as_bytes(*A_factor);
+        Bf = as_bytes(*B_factor);
+        TORCH_CHECK(Af.is_cuda() && Bf.is_cuda() && Af.numel() == M && Bf.numel() == E * N,
+                    "gemm_a4w4_grouped: factors must be device bytes of M and E*N entries");
+    }
+    auto out = torch::empty({Mpad, N}, torch::TensorOptions().dtype(torch::kBFloat16).device(A.device()));
+    check_status(mbs_gemm_a4w4_grouped_launch(
+                     Au.data_ptr<uint8_t>(), Bu.data_ptr<uint8_t>(), Asu.data_ptr<uint8_t>(),
+                     Bsu.data_ptr<uint8_t>(), Af.defined() ? Af.data_ptr<uint8_t>() : nullptr,
+                     Bf.defined() ? Bf.data_ptr<uint8_t>() : nullptr, goff.data_ptr<int32_t>(), (int)E,
+                     out.data_ptr(), (int)M, (int)N, (int)K, (int)Mpad, (int)snp, (int)config,
+                     current_stream(A)),
+                 "gemm_a4w4_grouped");
+    return out.narrow(0, 0, M);
+}
+
 std::string plan_name(int64_t M, int64_t N, int64_t K)
 {
     char buf[256];
@@ -330,6 +389,15 @@ PYBIND11_MODULE(mbs_gemm_a4w4, m)
           pybind11::arg("pad_byte") = 127);
     m.def("dequant_mxfp4", &dequant_mxfp4, "packed + shuffled scales -> fp32",
           pybind11::arg("packed"), pybind11::arg("scale"), pybind11::arg("b_preshuffled") = false);
+    m.def("gemm_a4w4_grouped", &gemm_a4w4_grouped,
+          "grouped (MoE) MXFP4 GEMM: expert e's rows of A times the e-th block of B",
+          pybind11::arg("A"), pybind11::arg("B"), pybind11::arg("A_scale"),
+          pybind11::arg("B_scale"), pybind11::arg("group_offsets"),
+          pybind11::arg("A_factor") = pybind11::none(), pybind11::arg("B_factor") = pybind11::none(),
+          pybind11::arg("config") = -1);
+    m.def("grouped_num_configs", []() { return mbs_gemm_a4w4_grouped_num_configs(); });
+    m.def("grouped_config_name",
+          [](int64_t c) { return std::string(mbs_gemm_a4w4_grouped_config_name((int)c)); });
     m.def("plan_name", &plan_name, "kernel plan the heuristic picks for (M, N, K)");
     m.def("num_configs", []() { return mbs_gemm_a4w4_num_configs(); });
     m.def("config_name", [](int64_t c) { return std::string(mbs_gemm_a4w4_config_name((int)c)); });

@@ -30,7 +30,14 @@ struct GemmArgs {
     int M, N, K, snp;   // snp = scaleN_pad
     int tiles_m, tiles_n;
     int splits, sps;    // K-splits and 128-K stages per split (even)
+    // Grouped (MoE) GEMM: expert e owns rows [groups[e], groups[e+1]) of A
+    // (multiples of 32) and the e-th [N, K/2] block of B, its scales and
+    // factors.  Null for a dense GEMM.
+    const int* groups;
+    int n_groups;
 };
+// Most experts a grouped launch takes (the per-expert tile table lives in LDS).
+constexpr int kMaxGroups = 1024;
 
 // ======================================================================
 // Tiled kernel
@@ -377,6 +384,8 @@ struct Unit {
     int split;     // K-split index
     int sbeg, nst; // first 128-K stage and number of stages of the split
     int valid;     // 0: past the end of this workgroup's unit list
+    int e;         // expert (grouped GEMM; 0 otherwise)
+    int rowlim;    // rows >= rowlim are not stored (the expert's or the matrix end)
 };
 
 // Chunk swizzle of an A pair slot: row r keeps its global 16-byte chunk c at
@@ -405,9 +414,15 @@ __device__ __forceinline__ int a_swz(int r) { return r & 7; }
 // scale reads are explicit ds_read instructions with counted lgkmcnt waits
 // (the compiler would otherwise make them wait for the A DMA into the
 // dynamically chosen slot).
-template <class T, bool GEN, bool SPLIT>
+//
+// GROUPED: the units are the tiles of every expert's row block (the tile
+// grid of expert e is ceil(rows_e / BM) x tiles_n); B, its scales and the B
+// factors are offset to expert e, and rows past the expert's end, which
+// belong to the next expert, are computed but not stored.
+template <class T, bool GEN, bool SPLIT, bool GROUPED = false>
 __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
 {
+    static_assert(!(GROUPED && SPLIT), "grouped GEMM runs without K splits");
     __shared__ __attribute__((aligned(1024))) uint8_t pa0[T::PSLOT];
     __shared__ __attribute__((aligned(1024))) uint8_t pa1[T::PSLOT];
     __shared__ __attribute__((aligned(1024))) uint8_t pa2[T::PSLOT];
@@ -439,7 +454,22 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     const int K = p.K, Kp = K >> 1;
     const int S_total = (K + 127) >> 7;
     const int n_st4 = (p.sps + 3) & ~3;
-    const int tiles = p.tiles_m * p.tiles_n;
+    // Grouped: the first M-tile index of each expert (prefix sums), in LDS.
+    __shared__ int gtile[GROUPED ? kMaxGroups + 1 : 1];
+    int tiles_m = p.tiles_m;
+    if constexpr (GROUPED) {
+        if (threadIdx.x == 0) {
+            int acc_t = 0;
+            for (int e = 0; e < p.n_groups; ++e) {
+                gtile[e] = acc_t;
+                acc_t += (p.groups[e + 1] - p.groups[e] + T::BM - 1) / T::BM;
+            }
+            gtile[p.n_groups] = acc_t;
+        }
+        __syncthreads();
+        tiles_m = gtile[p.n_groups];
+    }
+    const int tiles = tiles_m * p.tiles_n;
     const int units = tiles * p.splits;
     const int G = gridDim.x;
     // Workgroups are dispatched round-robin over the 8 XCDs (private L2s).
@@ -458,12 +488,29 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         constexpr int GROUP = 8;
         const int grp = t / (GROUP * p.tiles_n);
         const int first_m = grp * GROUP;
-        const int gsz = min(p.tiles_m - first_m, GROUP);
+        const int gsz = min(tiles_m - first_m, GROUP);
         const int tin = t - grp * GROUP * p.tiles_n;
-        u.m0 = (first_m + tin % gsz) * T::BM;
+        const int gm = first_m + tin % gsz;   // M-tile index
         u.n0 = (tin / gsz) * T::BN;
         u.sbeg = u.split * p.sps;
         u.nst = min(p.sps, S_total - u.sbeg);
+        if constexpr (GROUPED) {
+            // the expert of M-tile gm: the last e with gtile[e] <= gm
+            int lo = 0, hi = p.n_groups - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (gtile[mid] <= gm) lo = mid;
+                else hi = mid - 1;
+            }
+            u.e = lo;
+            u.m0 = p.groups[lo] + (gm - gtile[lo]) * T::BM;
+            // offsets are not checked on the host: never store past row M
+            u.rowlim = min(p.groups[lo + 1], p.M);
+        } else {
+            u.e = 0;
+            u.m0 = gm * T::BM;
+            u.rowlim = p.M;
+        }
         return u;
     };
 
@@ -471,10 +518,11 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     // the scalar offset, a dead stage uses soffset = kOOB (reads zeros).
     // The bounds keep every voffset + soffset below 2^32 (checked on the host).
     const int Mpad = (p.M + 31) & ~31, Npad = (p.N + 31) & ~31;
+    const int nexp = GROUPED ? p.n_groups : 1;   // stacked B blocks
     const rsrc_t rA = make_rsrc(p.A, (uint32_t)(p.M * Kp));
-    const rsrc_t rB = make_rsrc(p.B, (uint32_t)(p.N * Kp));
+    const rsrc_t rB = make_rsrc(p.B, (uint32_t)(nexp * p.N * Kp));
     const rsrc_t rAs = make_rsrc(p.As, (uint32_t)(Mpad * p.snp));
-    const rsrc_t rBs = make_rsrc(p.Bs, (uint32_t)(Npad * p.snp));
+    const rsrc_t rBs = make_rsrc(p.Bs, (uint32_t)(nexp * Npad * p.snp));
     int sa[2][T::SA], sb[2][T::SB];  // scale dwords of two groups (set = group & 1)
 
     // Per-lane offsets within a tile, fixed for the whole kernel.
@@ -560,9 +608,9 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     auto orig_of = [&](const Unit& un) __attribute__((always_inline)) {
         Orig o;
         o.a = un.valid ? (uint32_t)(un.m0 * Kp + un.sbeg * 64) : kOOB;
-        o.b = un.valid ? (uint32_t)(un.n0 * Kp + un.sbeg * 1024) : kOOB;
+        o.b = un.valid ? (uint32_t)((un.e * p.N + un.n0) * Kp + un.sbeg * 1024) : kOOB;
         o.as = un.valid ? (uint32_t)(un.m0 * p.snp + (un.sbeg >> 1) * 256) : kOOB;  // sbeg is even
-        o.bs = un.valid ? (uint32_t)(un.n0 * p.snp + (un.sbeg >> 1) * 256) : kOOB;
+        o.bs = un.valid ? (uint32_t)((un.e * Npad + un.n0) * p.snp + (un.sbeg >> 1) * 256) : kOOB;
         o.nst = un.valid ? un.nst : 0;
         o.sbeg = un.sbeg;
         return o;
@@ -836,21 +884,21 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     const bool has_f = (p.Af != nullptr) && (p.Bf != nullptr);
     const int Mdw = p.M & ~3;
     const rsrc_t rAf = make_rsrc(p.Af, has_f ? (uint32_t)Mdw : 0u);
-    const rsrc_t rBf = make_rsrc(p.Bf, has_f ? (uint32_t)p.N : 0u);
+    const rsrc_t rBf = make_rsrc(p.Bf, has_f ? (uint32_t)(nexp * p.N) : 0u);
     // Wave 0 loads the A bytes, wave NW-1-c the B chunk c (columns 256c..),
     // every other wave a filler.
     auto factor_dma = [&](const Unit& un, int par) __attribute__((always_inline)) {
         const bool go = has_f && un.valid;
         if constexpr (T::NW == 1) {
             dma4s(rAf, &fbytes[par][0], (uint32_t)(un.m0 + lane * 4), go ? 0u : kOOB);
-            dma4s(rBf, &fbytes[par][256], (uint32_t)(un.n0 + lane * 4), go ? 0u : kOOB);
+            dma4s(rBf, &fbytes[par][256], (uint32_t)(un.e * p.N + un.n0 + lane * 4), go ? 0u : kOOB);
         } else {
             const bool wa = w == 0;
             const int c = T::NW - 1 - w;            // B chunk of this wave
             const bool wb = !wa && c < T::NBC;
             uint8_t* dst = wa ? &fbytes[par][0] : (wb ? &fbytes[par][256 * (1 + c)] : fjunk);
             const rsrc_t r = wa ? rAf : rBf;
-            const uint32_t off = (uint32_t)((wa ? un.m0 : un.n0 + 256 * c) + lane * 4);
+            const uint32_t off = (uint32_t)((wa ? un.m0 : un.e * p.N + un.n0 + 256 * c) + lane * 4);
             dma4s(r, dst, off, go && (wa || wb) ? 0u : kOOB);
         }
     };
@@ -945,7 +993,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         });
 
         // ---- epilogue of unit `cur` -------------------------------------
-        const int rows_a = min(T::BM, p.M - cur.m0);
+        const int rows_a = max(0, min(T::BM, cur.rowlim - cur.m0));
         const int col_w = cur.n0 + wn * T::WN;
         if constexpr (SPLIT) {
             const rsrc_t rW = make_rsrc(p.ws + ((size_t)cur.split * p.M + cur.m0) * p.N,
@@ -1182,6 +1230,15 @@ hipError_t launch_bdirect(const GemmArgs& a, dim3 grid, bool gen, bool split, hi
     return hipGetLastError();
 }
 
+// Grouped (MoE) launches of the persistent kernel (no K splits).
+template <class T>
+hipError_t launch_bdirect_grouped(const GemmArgs& a, dim3 grid, bool gen, bool, hipStream_t s)
+{
+    if (gen) hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false, true>), grid, dim3(T::NT), 0, s, a);
+    else hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false, true>), grid, dim3(T::NT), 0, s, a);
+    return hipGetLastError();
+}
+
 template <int MT, int NF, int NWK, int U>
 hipError_t launch_skinny(const GemmArgs& a, dim3 grid, bool, bool split, hipStream_t s)
 {
@@ -1220,12 +1277,15 @@ using B128x256w14 = BdShape<128, 256, 1, 4>;
 #define MBS_BDIRECT_SHAPES_B(X) X(B64x256) X(B64x128) X(B64x64) X(B256x128w14)
 #define MBS_BDIRECT_SHAPES_C(X) X(B256x256w14) X(B192x256w14) X(B96x256w14)
 #define MBS_BDIRECT_SHAPES_D(X) X(B64x512w14) X(B128x384w14) X(B128x256w14)
+#define MBS_GROUPED_SHAPES(X) X(B256x256) X(B128x256w14) X(B64x256) X(B64x128)
 #define MBS_SKINNY_SHAPES(X) X(1, 2, 16, 4) X(2, 2, 16, 4) X(1, 2, 8, 8) X(2, 2, 8, 4) X(1, 1, 8, 8) X(2, 1, 8, 8)
 
 #define MBS_LAUNCH_SIG const GemmArgs&, dim3, bool, bool, hipStream_t
 #define MBS_TILED_INST(T) template hipError_t launch_tiled<T>(MBS_LAUNCH_SIG);
 #define MBS_BDIRECT_INST(T) template hipError_t launch_bdirect<T>(MBS_LAUNCH_SIG);
 #define MBS_SKINNY_INST(a, b, c, d) template hipError_t launch_skinny<a, b, c, d>(MBS_LAUNCH_SIG);
+#define MBS_GROUPED_INST(T) template hipError_t launch_bdirect_grouped<T>(MBS_LAUNCH_SIG);
+#define MBS_GROUPED_EXTERN(T) extern template hipError_t launch_bdirect_grouped<T>(MBS_LAUNCH_SIG);
 #define MBS_TILED_EXTERN(T) extern template hipError_t launch_tiled<T>(MBS_LAUNCH_SIG);
 #define MBS_BDIRECT_EXTERN(T) extern template hipError_t launch_bdirect<T>(MBS_LAUNCH_SIG);
 #define MBS_SKINNY_EXTERN(a, b, c, d) extern template hipError_t launch_skinny<a, b, c, d>(MBS_LAUNCH_SIG);
