@@ -65,6 +65,18 @@ int mbs_gemm_a4w4_launch(const uint8_t* A, const uint8_t* B, const uint8_t* ASca
                          int scaleN_pad, void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* mbs_gemm_a4w4_launch (config < 0) or mbs_gemm_a4w4_launch_config with an
+ * affine epilogue:  out[m][n] = bf16( C[m][n] * (alpha * f(AFactor[m]) *
+ * f(BFactor[n])) + bias[n] )  in fp32, bias bf16 [N] or NULL.  alpha = 1 with
+ * no bias gives exactly mbs_gemm_a4w4_launch's bytes.  The alpha/bias
+ * epilogue of the aiter assembly kernel the reference compares against
+ * (asm_vs_wg_kernel.md:85-87); the reference's own launcher has none. */
+int mbs_gemm_a4w4_launch_ex(int config, int splits, const uint8_t* A, const uint8_t* B,
+                            const uint8_t* AScale, const uint8_t* BScale, const uint8_t* AFactor,
+                            const uint8_t* BFactor, void* out, int M, int N, int K, int Mpad,
+                            int scaleN_pad, float alpha, const void* bias, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
 /* Grouped (mixture-of-experts) GEMM: E = num_groups experts share one launch.
  * Expert e owns rows [group_offsets[e], group_offsets[e+1]) of A (and of out)
  * and the e-th block of the stacked weights:

@@ -57,14 +57,17 @@ def clib() -> ctypes.CDLL:
     return _clib
 
 
-def gemm_a4w4(A, B, A_scale, B_scale, A_factor=None, B_factor=None):
+def gemm_a4w4(A, B, A_scale, B_scale, A_factor=None, B_factor=None, alpha: float = 1.0,
+              bias=None):
     """out[M,N] bf16 = dequant(A) @ dequant(B)^T [* f(A_factor)[:,None] * f(B_factor)[None,:]].
 
     Same contract as the reference's ``mbs_gemm_a4w4.gemm_a4w4``
     (interface/gemm_a4w4_pybind.cpp:19-64): A [M,K/2] fp4x2 row-major, B
     [N,K/2] fp4x2 preshuffled (16,16), shuffled E8M0 scales, optional u8
-    factors.  Asynchronous on the current stream."""
-    return ext().gemm_a4w4(A, B, A_scale, B_scale, A_factor, B_factor)
+    factors.  Asynchronous on the current stream.  Beyond the reference: an
+    affine epilogue, out = bf16(C * alpha * f(a) * f(b) + bias[n]) with bias a
+    bf16 [N] device tensor; the defaults leave the reference's result."""
+    return ext().gemm_a4w4(A, B, A_scale, B_scale, A_factor, B_factor, alpha, bias)
 
 
 def gemm_a4w4_grouped(A, B, A_scale, B_scale, group_offsets, A_factor=None, B_factor=None,

@@ -59,9 +59,16 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs p)
     f32x4 v = src[0];
     for (int s = 1; s < p.splits; ++s) v += *reinterpret_cast<const f32x4*>(p.ws + s * plane + (size_t)m * p.N + c);
     if (p.Af && p.Bf) {
-        const float fa = factor_of(p.Af[m]);
+        const float fa = factor_of(p.Af[m]) * p.alpha;
         const uint32_t bytes = *reinterpret_cast<const uint32_t*>(p.Bf + c);
         for (int k = 0; k < 4; ++k) v[k] = v[k] * (fa * factor_of(bytes >> (8 * k)));
+    } else if (p.alpha != 1.0f) {
+        for (int k = 0; k < 4; ++k) v[k] = v[k] * p.alpha;
+    }
+    if (p.bias) {
+        const uint32_t* bw = reinterpret_cast<const uint32_t*>(p.bias + c);
+        v[0] = add_nc(v[0], bf16_lo(bw[0])); v[1] = add_nc(v[1], bf16_hi(bw[0]));
+        v[2] = add_nc(v[2], bf16_lo(bw[1])); v[3] = add_nc(v[3], bf16_hi(bw[1]));
     }
     uint32_t* o = reinterpret_cast<uint32_t*>(p.out + (size_t)m * p.N + c);
     o[0] = pack_bf16x2(v[0], v[1]);
@@ -347,7 +354,8 @@ int validate(const uint8_t* A, const uint8_t* B, const uint8_t* As, const uint8_
 
 int run_plan(const Plan& pl, const uint8_t* A, const uint8_t* B, const uint8_t* As,
              const uint8_t* Bs, const uint8_t* Af, const uint8_t* Bf, void* out, int M, int N,
-             int K, int snp, void* ws, size_t ws_bytes, void* stream)
+             int K, int snp, void* ws, size_t ws_bytes, void* stream, float alpha = 1.0f,
+             const void* bias = nullptr)
 {
     const Config& c = kConfigs[pl.config];
     if (pl.ws_bytes > ws_bytes || (pl.ws_bytes && !ws))
@@ -362,6 +370,8 @@ int run_plan(const Plan& pl, const uint8_t* A, const uint8_t* B, const uint8_t* 
     a.tiles_n = (N + c.bn - 1) / c.bn;
     a.splits = pl.splits;
     a.sps = pl.sps;
+    a.alpha = alpha;
+    a.bias = static_cast<const uint16_t*>(bias);
     hipStream_t s = static_cast<hipStream_t>(stream);
     (void)hipGetLastError();  // do not report a stale error as ours
     // Persistent kernels take their general variant when a unit can have
@@ -440,6 +450,8 @@ int run_grouped(int g, const uint8_t* A, const uint8_t* B, const uint8_t* As, co
     split_stages(K, 1, &a.sps, &a.splits);
     a.groups = groups;
     a.n_groups = E;
+    a.alpha = 1.0f;
+    a.bias = nullptr;
     const int S_total = stages_of(K);
     const bool gen = (K % 128) != 0 || a.sps % 4 != 0 || S_total % a.sps != 0;
     const int units = grouped_units_bound(c, M, N, E);
@@ -564,6 +576,28 @@ int mbs_gemm_a4w4_launch_config(int config, int splits, const uint8_t* A, const 
                                         std::to_string(M));
     return run_plan(pl, A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, scaleN_pad,
                     workspace, workspace_bytes, stream);
+}
+
+int mbs_gemm_a4w4_launch_ex(int config, int splits, const uint8_t* A, const uint8_t* B,
+                            const uint8_t* AScale, const uint8_t* BScale, const uint8_t* AFactor,
+                            const uint8_t* BFactor, void* out, int M, int N, int K, int Mpad,
+                            int scaleN_pad, float alpha, const void* bias, void* workspace,
+                            size_t workspace_bytes, void* stream)
+{
+    set_last_error("");
+    int st = validate(A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, Mpad, scaleN_pad);
+    if (st != MBS_OK) return st;
+    if (!(alpha == alpha)) return fail(MBS_ERR_ARGUMENT, "alpha is NaN");
+    Plan pl;
+    if (config < 0) {
+        if (!choose_plan(M, N, K, workspace ? workspace_bytes : 0, &pl))
+            return fail(MBS_ERR_CONFIG, "no kernel configuration fits this problem");
+    } else if (!make_plan(config, splits, M, N, K, &pl)) {
+        return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) + " cannot run M=" +
+                                        std::to_string(M));
+    }
+    return run_plan(pl, A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, scaleN_pad,
+                    workspace, workspace_bytes, stream, alpha, bias);
 }
 
 }  // extern "C"

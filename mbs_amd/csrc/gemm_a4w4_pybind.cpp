@@ -97,7 +97,8 @@ Operands prepare(const at::Tensor& A, const at::Tensor& B, const at::Tensor& A_s
     return o;
 }
 
-at::Tensor run(const Operands& o, int config, int splits)
+at::Tensor run(const Operands& o, int config, int splits, double alpha = 1.0,
+               const c10::optional<at::Tensor>& bias = c10::nullopt)
 {
     c10::DeviceGuard guard(o.A.device());
     auto out = torch::empty({o.Mpad, o.N},
@@ -110,7 +111,21 @@ at::Tensor run(const Operands& o, int config, int splits)
     const uint8_t* bf = o.factors ? o.Bf.data_ptr<uint8_t>() : nullptr;
     void* s = current_stream(o.A);
     int st;
-    if (config < 0)
+    at::Tensor bu;
+    if (bias.has_value()) {
+        TORCH_CHECK(bias->is_cuda() && bias->device() == o.A.device() &&
+                        bias->scalar_type() == at::kBFloat16 && bias->numel() == o.N,
+                    "gemm_a4w4: bias must be a bf16 device tensor of N entries");
+        bu = bias->contiguous();
+    }
+    if (alpha != 1.0 || bu.defined())
+        st = mbs_gemm_a4w4_launch_ex(config, splits, o.A.data_ptr<uint8_t>(),
+                                     o.B.data_ptr<uint8_t>(), o.As.data_ptr<uint8_t>(),
+                                     o.Bs.data_ptr<uint8_t>(), af, bf, out.data_ptr(), o.M, o.N,
+                                     o.K, o.Mpad, o.snp, (float)alpha,
+                                     bu.defined() ? bu.data_ptr() : nullptr,
+                                     ws ? wst.data_ptr() : nullptr, ws, s);
+    else if (config < 0)
         st = mbs_gemm_a4w4_launch(o.A.data_ptr<uint8_t>(), o.B.data_ptr<uint8_t>(),
                                   o.As.data_ptr<uint8_t>(), o.Bs.data_ptr<uint8_t>(), af, bf,
                                   out.data_ptr(), o.M, o.N, o.K, o.Mpad, o.snp,
@@ -129,20 +144,23 @@ at::Tensor run(const Operands& o, int config, int splits)
 
 // The reference's operator (interface/gemm_a4w4_pybind.cpp:19-64).
 at::Tensor gemm_a4w4(at::Tensor A, at::Tensor B, at::Tensor A_scale, at::Tensor B_scale,
-                     c10::optional<at::Tensor> A_factor, c10::optional<at::Tensor> B_factor)
+                     c10::optional<at::Tensor> A_factor, c10::optional<at::Tensor> B_factor,
+                     double alpha, c10::optional<at::Tensor> bias)
 {
-    return run(prepare(A, B, A_scale, B_scale, A_factor, B_factor), -1, 0);
+    return run(prepare(A, B, A_scale, B_scale, A_factor, B_factor), -1, 0, alpha, bias);
 }
 
 // Same operator with a forced kernel configuration (tests, tuning).
 at::Tensor gemm_a4w4_config(int64_t config, int64_t splits, at::Tensor A, at::Tensor B,
                             at::Tensor A_scale, at::Tensor B_scale,
                             c10::optional<at::Tensor> A_factor,
-                            c10::optional<at::Tensor> B_factor)
+                            c10::optional<at::Tensor> B_factor, double alpha,
+                            c10::optional<at::Tensor> bias)
 {
     TORCH_CHECK(config >= 0 && config < mbs_gemm_a4w4_num_configs(), "gemm_a4w4_config: config ",
                 config, " out of range [0, ", mbs_gemm_a4w4_num_configs(), ")");
-    return run(prepare(A, B, A_scale, B_scale, A_factor, B_factor), (int)config, (int)splits);
+    return run(prepare(A, B, A_scale, B_scale, A_factor, B_factor), (int)config, (int)splits,
+               alpha, bias);
 }
 
 // bf16 [R, K] -> (packed u8 [R, K/2], scales).  shuffle=True returns the
@@ -363,14 +381,17 @@ PYBIND11_MODULE(mbs_gemm_a4w4, m)
 {
     m.doc() = "MI355X (gfx950) MXFP4 A4W4 GEMM";
     m.def("gemm_a4w4", &gemm_a4w4,
-          "MXFP4 A4W4 GEMM: out[M,N] = dequant(A) @ dequant(B)^T [* f(A_factor) * f(B_factor)^T]",
+          "MXFP4 A4W4 GEMM: out[M,N] = dequant(A) @ dequant(B)^T [* alpha * f(A_factor) * "
+          "f(B_factor)^T] [+ bias]",
           pybind11::arg("A"), pybind11::arg("B"), pybind11::arg("A_scale"),
           pybind11::arg("B_scale"), pybind11::arg("A_factor") = pybind11::none(),
-          pybind11::arg("B_factor") = pybind11::none());
+          pybind11::arg("B_factor") = pybind11::none(), pybind11::arg("alpha") = 1.0,
+          pybind11::arg("bias") = pybind11::none());
     m.def("gemm_a4w4_config", &gemm_a4w4_config, "gemm_a4w4 with a forced kernel configuration",
           pybind11::arg("config"), pybind11::arg("splits"), pybind11::arg("A"), pybind11::arg("B"),
           pybind11::arg("A_scale"), pybind11::arg("B_scale"),
-          pybind11::arg("A_factor") = pybind11::none(), pybind11::arg("B_factor") = pybind11::none());
+          pybind11::arg("A_factor") = pybind11::none(), pybind11::arg("B_factor") = pybind11::none(),
+          pybind11::arg("alpha") = 1.0, pybind11::arg("bias") = pybind11::none());
     m.def("quantize_mxfp4", &quantize_mxfp4, "bf16 -> (packed e2m1, E8M0 scales)",
           pybind11::arg("x"), pybind11::arg("shuffle") = true, pybind11::arg("pad_byte") = 127);
     m.def("quantize_mxfp4_mbs", &quantize_mxfp4_mbs,

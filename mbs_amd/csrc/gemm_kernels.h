@@ -35,9 +35,19 @@ struct GemmArgs {
     // factors.  Null for a dense GEMM.
     const int* groups;
     int n_groups;
+    // Epilogue: out = bf16(acc * (alpha * f(a) * f(b)) + bias[n]); alpha 1 and
+    // no bias leave the plain product.  bias: bf16 [N] (grouped: [E][N]) or null.
+    float alpha;
+    const uint16_t* bias;
 };
 // Most experts a grouped launch takes (the per-expert tile table lives in LDS).
 constexpr int kMaxGroups = 1024;
+
+// Whether the bf16 epilogue has anything beyond the plain conversion.
+inline bool affine_epilogue(const GemmArgs& a)
+{
+    return (a.Af != nullptr && a.Bf != nullptr) || a.bias != nullptr || a.alpha != 1.0f;
+}
 
 // ======================================================================
 // Tiled kernel
@@ -311,20 +321,28 @@ __global__ void __launch_bounds__(T::NT) gemm_tiled_kernel(const GemmArgs p)
     } else {
         const rsrc_t rAf = make_rsrc(p.Af + m0, has_f ? (uint32_t)rows_a : 0u);
         const rsrc_t rBf = make_rsrc(p.Bf, has_f ? (uint32_t)p.N : 0u);
+        const rsrc_t rBias = make_rsrc(p.bias, p.bias ? (uint32_t)(p.N * 2) : 0u);
         const rsrc_t rO = make_rsrc(p.out + (size_t)m0 * p.N, (uint32_t)(rows_a * p.N * 2));
         float fa[T::FM];
         static_for<T::FM>([&](auto i) {
-            fa[i] = has_f ? factor_of(load1(rAf, row_l + i * 16)) : 1.0f;
+            fa[i] = (has_f ? factor_of(load1(rAf, row_l + i * 16)) : 1.0f) * p.alpha;
         });
         static_for<T::FN>([&](auto j) {
             const int c = col_w + j * 16;
             if (c < p.N) {
                 const uint32_t bytes = (uint32_t)load4(rBf, c + colq);
-                float fb[4];
+                float fb[4], bz[4] = {0.f, 0.f, 0.f, 0.f};
                 for (int q = 0; q < 4; ++q) fb[q] = has_f ? factor_of(bytes >> (8 * q)) : 1.0f;
+                if (p.bias) {
+                    const i32x2 bw = load8(rBias, (uint32_t)((c + colq) * 2));
+                    bz[0] = bf16_lo((uint32_t)bw[0]); bz[1] = bf16_hi((uint32_t)bw[0]);
+                    bz[2] = bf16_lo((uint32_t)bw[1]); bz[3] = bf16_hi((uint32_t)bw[1]);
+                }
                 static_for<T::FM>([&](auto i) {
                     f32x4 v = acc[i][j];
                     for (int q = 0; q < 4; ++q) v[q] = v[q] * (fa[i] * fb[q]);
+                    if (p.bias)
+                        for (int q = 0; q < 4; ++q) v[q] = add_nc(v[q], bz[q]);
                     store8(rO, (uint32_t)(((row_l + i * 16) * p.N + c + colq) * 2),
                            pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
                 });
@@ -371,6 +389,10 @@ struct BdShape {
     // NBC chunks of 256 after them.
     static constexpr int NBC = (BN + 255) / 256;
     static constexpr int FBW = 256 * (1 + NBC);
+    // Epilogue bias of a unit in LDS: NBB chunks of 128 bf16 columns, one
+    // 256-byte DMA each, FBB per wave.
+    static constexpr int NBB = (BN + 127) / 128;
+    static constexpr int FBB = (NBB + NW - 1) / NW;
     static_assert(BM <= 256, "one 256-byte chunk of A factor bytes");
     static_assert(NW == 1 ? NBC == 1 : NW >= 1 + NBC, "one factor DMA per wave");
     static_assert(BM % 16 == 0, "pair halves of whole 8-row DMA groups");
@@ -419,21 +441,30 @@ __device__ __forceinline__ int a_swz(int r) { return r & 7; }
 // grid of expert e is ceil(rows_e / BM) x tiles_n); B, its scales and the B
 // factors are offset to expert e, and rows past the expert's end, which
 // belong to the next expert, are computed but not stored.
-template <class T, bool GEN, bool SPLIT, bool GROUPED = false>
+//
+// AFF: the bf16 epilogue applies MBS factors, alpha and the column bias.  It
+// is a separate instantiation so that the plain epilogue's register
+// allocation is not sized for the scaled one's extra live values (which
+// would spill into scratch, and each scratch reload waits on the next
+// unit's outstanding DMAs).
+template <class T, bool GEN, bool SPLIT, bool GROUPED = false, bool AFF = false>
 __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
 {
     static_assert(!(GROUPED && SPLIT), "grouped GEMM runs without K splits");
+    static_assert(!(AFF && SPLIT), "split launches write fp32 partial sums");
     __shared__ __attribute__((aligned(1024))) uint8_t pa0[T::PSLOT];
     __shared__ __attribute__((aligned(1024))) uint8_t pa1[T::PSLOT];
     __shared__ __attribute__((aligned(1024))) uint8_t pa2[T::PSLOT];
     // MBS factor bytes of a unit (A rows at [0,256), B columns at [256,512)),
     // double-buffered by unit parity, and the byte -> fp32 factor table.
     __shared__ __attribute__((aligned(16))) uint8_t fbytes[2][T::FBW];
+    __shared__ __attribute__((aligned(16))) uint16_t fbias[2][T::NBB * 128];
     __shared__ __attribute__((aligned(16))) uint8_t fjunk[1024];  // target of filler DMAs
     // Scale groups, double-buffered by group parity.
     __shared__ __attribute__((aligned(1024))) uint8_t sc0[T::SBUF];
     __shared__ __attribute__((aligned(1024))) uint8_t sc1[T::SBUF];
     __shared__ float ftab[256];
+    __shared__ uint32_t ftail;   // A factor bytes of rows Mdw.. M-1 (at most 3)
     // Pair slots of the current 4-stage iteration: q0 (pair 0, stages 0-1),
     // q1 (pair 1, stages 2-3), q2 (pair 2, DMA'd by stages 0-1); pair 3 (DMA'd
     // by stages 2-3) reuses q0.  Next iteration: (q0, q1, q2) <- (q2, q0, q1).
@@ -701,7 +732,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     // next unit (FD per wave).  vmcnt retires in issue order, so the first
     // wait after an epilogue can leave them in flight (SPLIT: its fp32
     // partial stores exceed the 6-bit count and are waited for).
-    constexpr int FD = T::NW == 1 ? 2 : 1;
+    constexpr int FD = (T::NW == 1 ? 2 : 1) + T::FBB;   // factor + bias DMAs per wave
     constexpr int EPI_OPS = SPLIT ? 0 : T::FM * (T::FN / 2) + FD;
     static_assert(NI_EVEN + EPI_OPS <= 63 && NI_ODD <= 63, "vmcnt is 6 bits");
 
@@ -880,7 +911,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     // wave issues exactly FD DMAs, the others (and every DMA without factors
     // or past the last unit) read out of range into fjunk, so the count is
     // the same for all waves and units.  The A range is cut to whole dwords;
-    // the at most 3 rows past it are read directly in the epilogue.
+    // the bytes of the at most 3 rows past it are read once, into ftail.
     const bool has_f = (p.Af != nullptr) && (p.Bf != nullptr);
     const int Mdw = p.M & ~3;
     const rsrc_t rAf = make_rsrc(p.Af, has_f ? (uint32_t)Mdw : 0u);
@@ -902,10 +933,39 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             dma4s(r, dst, off, go && (wa || wb) ? 0u : kOOB);
         }
     };
-    if (has_f) {
-        for (int b = threadIdx.x; b < 256; b += T::NT) ftab[b] = factor_of((uint32_t)b);
+    // Epilogue bias of a unit's columns -> fbias[par] (FBB DMAs per wave,
+    // fillers into fjunk when there is no bias or no unit).
+    const bool has_bias = p.bias != nullptr;
+    if constexpr (AFF) {
+        // The scaled epilogue reads its operands without branches: factor
+        // 1.0 for every byte without factors, a bias of -0.0 (x + -0.0 == x,
+        // signed zeros included) without a bias.  These writes are ordered
+        // before the first epilogue by the prologue's barrier.
+        for (int b = threadIdx.x; b < 256; b += T::NT) ftab[b] = has_f ? factor_of((uint32_t)b) : 1.0f;
+        if (threadIdx.x == 0) {
+            uint32_t t = 0;
+            if (has_f) {
+                const rsrc_t rAt = make_rsrc(p.Af, (uint32_t)p.M);
+                for (int k = 0; k < p.M - Mdw; ++k) t |= (load1(rAt, (uint32_t)(Mdw + k)) & 255u) << (8 * k);
+            }
+            ftail = t;
+        }
+        if (!has_bias) {
+            uint32_t* fb = reinterpret_cast<uint32_t*>(&fbias[0][0]);
+            for (int k = threadIdx.x; k < T::NBB * 128; k += T::NT) fb[k] = 0x80008000u;
+        }
     }
+    const rsrc_t rBias = make_rsrc(p.bias, has_bias ? (uint32_t)(nexp * p.N * 2) : 0u);
+    auto bias_dma = [&](const Unit& un, int par) __attribute__((always_inline)) {
+        static_for<T::FBB>([&](auto I) {
+            const int k = w + T::NW * decltype(I)::value;   // 128-column chunk
+            const bool go = has_bias && un.valid && k < T::NBB;
+            dma4s(rBias, go ? (uint8_t*)&fbias[par][k * 128] : fjunk,
+                  (uint32_t)((un.e * p.N + un.n0 + k * 128) * 2 + lane * 4), go ? 0u : kOOB);
+        });
+    };
     factor_dma(cur, 0);
+    bias_dma(cur, 0);
 
     // ---- prologue: scale groups 0 and 1, A pair 0, B stage 0, A pair 1,
     // B stages 1 and 2 of the first unit (pair p is what local stage 2p-4
@@ -993,10 +1053,13 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         });
 
         // ---- epilogue of unit `cur` -------------------------------------
-        const int rows_a = max(0, min(T::BM, cur.rowlim - cur.m0));
+        // (read back as scalars: the store descriptors must be uniform, or
+        // every store becomes a readfirstlane loop)
+        const int m0u = __builtin_amdgcn_readfirstlane(cur.m0);
+        const int rows_a = __builtin_amdgcn_readfirstlane(max(0, min(T::BM, cur.rowlim - cur.m0)));
         const int col_w = cur.n0 + wn * T::WN;
         if constexpr (SPLIT) {
-            const rsrc_t rW = make_rsrc(p.ws + ((size_t)cur.split * p.M + cur.m0) * p.N,
+            const rsrc_t rW = make_rsrc(p.ws + ((size_t)cur.split * p.M + m0u) * p.N,
                                         (uint32_t)(rows_a * p.N * 4));
             static_for<T::FN>([&](auto j) {
                 const int c = col_w + j * 16;
@@ -1007,21 +1070,26 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                 }
             });
         } else {
-            const rsrc_t rO = make_rsrc(p.out + (size_t)cur.m0 * p.N, (uint32_t)(rows_a * p.N * 2));
-            // HF: with MBS factors (out = C * (f(a_m) * f(b_n))); without them
-            // the accumulators are converted as they are.
+            const rsrc_t rO = make_rsrc(p.out + (size_t)m0u * p.N, (uint32_t)(rows_a * p.N * 2));
+            // HF: scaled and shifted, out = C * (alpha * f(a_m) * f(b_n)) +
+            // bias[n], with the table and bias set up for the cases without
+            // factors or bias.  Otherwise the accumulators are converted as
+            // they are.
             auto epi = [&](auto HF) __attribute__((always_inline)) {
                 constexpr bool hf = decltype(HF)::value;
                 float fa[T::FM];
                 if constexpr (hf) {
-                    static_for<T::FM>([&](auto i) { fa[i] = ftab[fbytes[par][row_l + i * 16]]; });
-                    if (cur.m0 + T::BM > Mdw) {  // rows past the whole-dword range
-                        const rsrc_t rAf1 = make_rsrc(p.Af, (uint32_t)p.M);
-                        static_for<T::FM>([&](auto i) {
-                            const int r = cur.m0 + row_l + i * 16;
-                            if (r >= Mdw && r < p.M) fa[i] = factor_of(load1(rAf1, (uint32_t)r));
-                        });
-                    }
+                    const uint32_t tail = ftail;
+                    static_for<T::FM>([&](auto i) {
+                        const int r = m0u + row_l + i * 16;
+                        const uint32_t bt = (tail >> (8 * ((r - Mdw) & 3))) & 255u;
+                        // read unconditionally: a read under the select becomes
+                        // a branch, which splits the epilogue into blocks
+                        uint32_t bd = fbytes[par][row_l + i * 16];
+                        asm volatile("" : "+v"(bd));
+                        const uint32_t b = r >= Mdw ? bt : bd;
+                        fa[i] = ftab[b] * p.alpha;
+                    });
                 }
                 // Fragment pair (2p, 2p+1) covers 32 columns.  Lane (m, q) holds
                 // columns 4q..4q+3 of each; after the swaps it holds 8 consecutive
@@ -1031,25 +1099,32 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                 static_for<T::FN / 2>([&](auto P2) {
                     constexpr int j0 = 2 * decltype(P2)::value;
                     const int c = col_w + j0 * 16;
-                    float f0[4], f1[4];
+                    float f0[4], f1[4], z0[4], z1[4];
+                    const int cl = wn * T::WN + j0 * 16 + q * 4;   // lane's first column in the tile
                     if constexpr (hf) {
-                        const int cl = wn * T::WN + j0 * 16 + q * 4;
                         const uint32_t b0 = *reinterpret_cast<const uint32_t*>(&fbytes[par][256 + cl]);
                         const uint32_t b1 = *reinterpret_cast<const uint32_t*>(&fbytes[par][256 + cl + 16]);
-                        for (int k = 0; k < 4; ++k) {
+                        static_for<4>([&](auto K4) {
+                            constexpr int k = decltype(K4)::value;
                             f0[k] = ftab[(b0 >> (8 * k)) & 255];
                             f1[k] = ftab[(b1 >> (8 * k)) & 255];
-                        }
+                        });
+                        const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&fbias[par][cl]);
+                        const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&fbias[par][cl + 16]);
+                        const uint32_t u0 = w0[0], u1 = w0[1], u2 = w1[0], u3 = w1[1];
+                        z0[0] = bf16_lo(u0); z0[1] = bf16_hi(u0); z0[2] = bf16_lo(u1); z0[3] = bf16_hi(u1);
+                        z1[0] = bf16_lo(u2); z1[1] = bf16_hi(u2); z1[2] = bf16_lo(u3); z1[3] = bf16_hi(u3);
                     }
                     // N % 16 == 0: the pair is all in, only its first half, or out
                     const bool store_ok = c < p.N && (c + 16 < p.N || q < 2);
                     static_for<T::FM>([&](auto i) {
                         f32x4 v0 = acc[i][j0], v1 = acc[i][j0 + 1];
                         if constexpr (hf) {
-                            for (int k = 0; k < 4; ++k) {
-                                v0[k] = v0[k] * (fa[i] * f0[k]);
-                                v1[k] = v1[k] * (fa[i] * f1[k]);
-                            }
+                            static_for<4>([&](auto K4) {
+                                constexpr int k = decltype(K4)::value;
+                                v0[k] = add_nc(v0[k] * (fa[i] * f0[k]), z0[k]);
+                                v1[k] = add_nc(v1[k] * (fa[i] * f1[k]), z1[k]);
+                            });
                         }
                         uint32_t x0 = pack_bf16x2(v0[0], v0[1]), x1 = pack_bf16x2(v0[2], v0[3]);
                         uint32_t y0 = pack_bf16x2(v1[0], v1[1]), y1 = pack_bf16x2(v1[2], v1[3]);
@@ -1068,11 +1143,11 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                     });
                 });
             };
-            if (has_f) epi(std::true_type{});
-            else epi(std::false_type{});
+            epi(std::integral_constant<bool, AFF>{});
         }
         par ^= 1;
         factor_dma(nxt, par);
+        bias_dma(nxt, par);
         cur = nxt;
         nxt = unit_of(id + 2 * G);
         ocur = onxt;
@@ -1194,9 +1269,17 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
         if (p.Af && p.Bf) {
             const rsrc_t rAf = make_rsrc(p.Af, (uint32_t)p.M);
             const rsrc_t rBf = make_rsrc(p.Bf, (uint32_t)p.N);
-            const float fa = factor_of(load1(rAf, row));
+            const float fa = factor_of(load1(rAf, row)) * p.alpha;
             const uint32_t bytes = (uint32_t)load4(rBf, c);
             for (int q = 0; q < 4; ++q) v[q] = v[q] * (fa * factor_of(bytes >> (8 * q)));
+        } else if (p.alpha != 1.0f) {
+            for (int q = 0; q < 4; ++q) v[q] = v[q] * p.alpha;
+        }
+        if (p.bias) {
+            const rsrc_t rBias = make_rsrc(p.bias, (uint32_t)(p.N * 2));
+            const i32x2 bw = load8(rBias, (uint32_t)(c * 2));
+            v[0] = add_nc(v[0], bf16_lo((uint32_t)bw[0])); v[1] = add_nc(v[1], bf16_hi((uint32_t)bw[0]));
+            v[2] = add_nc(v[2], bf16_lo((uint32_t)bw[1])); v[3] = add_nc(v[3], bf16_hi((uint32_t)bw[1]));
         }
         const rsrc_t rO = make_rsrc(p.out, (uint32_t)(p.M * p.N * 2));
         store8(rO, (uint32_t)((row * p.N + c) * 2), pack_bf16x2(v[0], v[1]),
@@ -1220,11 +1303,14 @@ hipError_t launch_tiled(const GemmArgs& a, dim3 grid, bool ktail, bool split, hi
 template <class T>
 hipError_t launch_bdirect(const GemmArgs& a, dim3 grid, bool gen, bool split, hipStream_t s)
 {
+    const bool aff = affine_epilogue(a);
     if (gen) {
         if (split) hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, true>), grid, dim3(T::NT), 0, s, a);
+        else if (aff) hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false, false, true>), grid, dim3(T::NT), 0, s, a);
         else hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false>), grid, dim3(T::NT), 0, s, a);
     } else {
         if (split) hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, true>), grid, dim3(T::NT), 0, s, a);
+        else if (aff) hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false, false, true>), grid, dim3(T::NT), 0, s, a);
         else hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false>), grid, dim3(T::NT), 0, s, a);
     }
     return hipGetLastError();
@@ -1234,8 +1320,14 @@ hipError_t launch_bdirect(const GemmArgs& a, dim3 grid, bool gen, bool split, hi
 template <class T>
 hipError_t launch_bdirect_grouped(const GemmArgs& a, dim3 grid, bool gen, bool, hipStream_t s)
 {
-    if (gen) hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false, true>), grid, dim3(T::NT), 0, s, a);
-    else hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false, true>), grid, dim3(T::NT), 0, s, a);
+    const bool aff = affine_epilogue(a);
+    if (gen) {
+        if (aff) hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false, true, true>), grid, dim3(T::NT), 0, s, a);
+        else hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false, true>), grid, dim3(T::NT), 0, s, a);
+    } else {
+        if (aff) hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false, true, true>), grid, dim3(T::NT), 0, s, a);
+        else hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false, true>), grid, dim3(T::NT), 0, s, a);
+    }
     return hipGetLastError();
 }
 

@@ -91,6 +91,10 @@ __device__ __forceinline__ i32x4 load16nt(rsrc_t r, uint32_t voffset)
 {
     return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 2));
 }
+__device__ __forceinline__ i32x2 load8(rsrc_t r, uint32_t voffset)
+{
+    return __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voffset, 0, 0));
+}
 __device__ __forceinline__ int load4(rsrc_t r, uint32_t voffset)
 {
     return (int)__builtin_amdgcn_raw_buffer_load_b32(r, voffset, 0, 0);
@@ -306,6 +310,17 @@ struct FactorTable {
 };
 
 // ------------------------------------------------------------ bf16 pack
+// x + y rounded on its own: never fused with the product that feeds it
+// (the epilogue bias add has a defined fp32 order: multiply, round, add).
+__device__ __forceinline__ float add_nc(float x, float y)
+{
+#pragma clang fp contract(off)
+    return x + y;
+}
+// bf16 bits (low or high half of a dword) -> fp32, exactly.
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
 // Two fp32 -> packed bf16x2, round to nearest even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
 {

@@ -258,6 +258,28 @@ def epilogue_bf16(c, a_factor=None, b_factor=None) -> np.ndarray:
     return out
 
 
+def epilogue_affine_bf16(c, a_factor=None, b_factor=None, alpha: float = 1.0,
+                        bias_bits=None) -> np.ndarray:
+    """The affine epilogue (no reference counterpart in its own launcher; the
+    aiter assembly kernel it benchmarks against has alpha and bias,
+    asm_vs_wg_kernel.md:85-87): in fp32, c * ((f(a)[m] * alpha) * f(b)[n]),
+    plus bias[n] (bf16 bits) when given, then bf16 RNE (uint16 bits).  The
+    factors are 1 when absent.  With alpha 1 and no bias this is
+    epilogue_bf16."""
+    c = np.ascontiguousarray(c, dtype=np.float32)
+    M, N = c.shape
+    fa = (mbs_factor(np.asarray(a_factor, np.uint8).reshape(-1)) if a_factor is not None
+          else np.ones(M, np.float32)).astype(np.float32)
+    fb = (mbs_factor(np.asarray(b_factor, np.uint8).reshape(-1)) if b_factor is not None
+          else np.ones(N, np.float32)).astype(np.float32)
+    sa = (fa * np.float32(alpha)).astype(np.float32)
+    v = (c * (sa[:, None] * fb[None, :]).astype(np.float32)).astype(np.float32)
+    if bias_bits is not None:
+        b = (np.asarray(bias_bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+        v = (v + b[None, :]).astype(np.float32)
+    return f32_to_bf16_bits(v)
+
+
 def run_torch(x_packed, w_packed, x_scales, w_scales, a_factor=None, b_factor=None,
               threads: int | None = None):
     """Restatement of run_torch / run_torch_mbs (test_gemm_a4w4.py:28-44,54-69).
