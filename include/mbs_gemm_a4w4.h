@@ -97,6 +97,16 @@ int mbs_gemm_a4w4_grouped_launch(const uint8_t* A, const uint8_t* B, const uint8
                                  const uint8_t* BFactor, const int* group_offsets, int num_groups,
                                  void* out, int M, int N, int K, int Mpad, int scaleN_pad,
                                  int config, void* stream);
+/* mbs_gemm_a4w4_grouped_launch with the affine epilogue of
+ * mbs_gemm_a4w4_launch_ex: expert e's rows get
+ * bf16(C * (alpha * f(a) * f(b)) + bias[e][n]); bias is bf16 [E][N] or NULL.
+ * No counterpart in the reference. */
+int mbs_gemm_a4w4_grouped_launch_ex(const uint8_t* A, const uint8_t* B, const uint8_t* AScale,
+                                    const uint8_t* BScale, const uint8_t* AFactor,
+                                    const uint8_t* BFactor, const int* group_offsets,
+                                    int num_groups, void* out, int M, int N, int K, int Mpad,
+                                    int scaleN_pad, float alpha, const void* bias, int config,
+                                    void* stream);
 int mbs_gemm_a4w4_grouped_num_configs(void);
 const char* mbs_gemm_a4w4_grouped_config_name(int config);
 

@@ -71,7 +71,7 @@ def gemm_a4w4(A, B, A_scale, B_scale, A_factor=None, B_factor=None, alpha: float
 
 
 def gemm_a4w4_grouped(A, B, A_scale, B_scale, group_offsets, A_factor=None, B_factor=None,
-                      config: int = -1):
+                      config: int = -1, alpha: float = 1.0, bias=None):
     """Grouped (mixture-of-experts) GEMM in one launch.
 
     Expert e owns rows [group_offsets[e], group_offsets[e+1]) of A and of the
@@ -79,9 +79,11 @@ def gemm_a4w4_grouped(A, B, A_scale, B_scale, group_offsets, A_factor=None, B_fa
     [E*N, K/2]), its shuffled scale block and its N factor bytes.  Offsets are
     int32 [E+1]: 0 first, non-decreasing multiples of 32 (pad each expert's
     token block), last <= M.  Each expert's rows equal ``gemm_a4w4`` of that
-    expert alone.  Rows past the last offset are not written."""
+    expert alone.  Rows past the last offset are not written.  ``alpha`` and
+    ``bias`` (bf16 [E, N] or [E*N], expert e's row added to its rows) give the
+    affine epilogue of ``gemm_a4w4``."""
     return ext().gemm_a4w4_grouped(A, B, A_scale, B_scale, group_offsets, A_factor, B_factor,
-                                   config)
+                                   config, alpha, bias)
 
 
 def quantize_mxfp4(x, shuffle: bool = True, pad_byte: int = 127):

@@ -438,7 +438,7 @@ int choose_grouped(int M, int N, int K, int E)
 
 int run_grouped(int g, const uint8_t* A, const uint8_t* B, const uint8_t* As, const uint8_t* Bs,
                 const uint8_t* Af, const uint8_t* Bf, const int* groups, int E, void* out, int M,
-                int N, int K, int snp, void* stream)
+                int N, int K, int snp, void* stream, float alpha, const void* bias)
 {
     const Config& c = kConfigs[config_index(kGrouped[g].dense)];
     GemmArgs a{};
@@ -450,8 +450,8 @@ int run_grouped(int g, const uint8_t* A, const uint8_t* B, const uint8_t* As, co
     split_stages(K, 1, &a.sps, &a.splits);
     a.groups = groups;
     a.n_groups = E;
-    a.alpha = 1.0f;
-    a.bias = nullptr;
+    a.alpha = alpha;
+    a.bias = static_cast<const uint16_t*>(bias);
     const int S_total = stages_of(K);
     const bool gen = (K % 128) != 0 || a.sps % 4 != 0 || S_total % a.sps != 0;
     const int units = grouped_units_bound(c, M, N, E);
@@ -512,6 +512,18 @@ int mbs_gemm_a4w4_grouped_launch(const uint8_t* A, const uint8_t* B, const uint8
                                  void* out, int M, int N, int K, int Mpad, int scaleN_pad,
                                  int config, void* stream)
 {
+    return mbs_gemm_a4w4_grouped_launch_ex(A, B, AScale, BScale, AFactor, BFactor, group_offsets,
+                                           num_groups, out, M, N, K, Mpad, scaleN_pad, 1.0f, nullptr,
+                                           config, stream);
+}
+
+int mbs_gemm_a4w4_grouped_launch_ex(const uint8_t* A, const uint8_t* B, const uint8_t* AScale,
+                                    const uint8_t* BScale, const uint8_t* AFactor,
+                                    const uint8_t* BFactor, const int* group_offsets,
+                                    int num_groups, void* out, int M, int N, int K, int Mpad,
+                                    int scaleN_pad, float alpha, const void* bias, int config,
+                                    void* stream)
+{
     set_last_error("");
     int st = validate(A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, Mpad, scaleN_pad);
     if (st != MBS_OK) return st;
@@ -524,9 +536,10 @@ int mbs_gemm_a4w4_grouped_launch(const uint8_t* A, const uint8_t* B, const uint8
         return fail(MBS_ERR_ARGUMENT, "stacked expert weights too large for 32-bit buffer offsets");
     if (config < -1 || config >= kNumGrouped)
         return fail(MBS_ERR_CONFIG, "grouped config out of range");
+    if (!(alpha == alpha)) return fail(MBS_ERR_ARGUMENT, "alpha is NaN");
     const int g = config >= 0 ? config : choose_grouped(M, N, K, num_groups);
     return run_grouped(g, A, B, AScale, BScale, AFactor, BFactor, group_offsets, num_groups, out, M,
-                       N, K, scaleN_pad, stream);
+                       N, K, scaleN_pad, stream, alpha, bias);
 }
 
 int mbs_gemm_a4w4_grouped_num_configs(void) { return kNumGrouped; }

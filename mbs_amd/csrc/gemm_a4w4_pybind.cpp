@@ -318,7 +318,8 @@ at::Tensor dequant_mxfp4(at::Tensor packed, at::Tensor scale_shuffled, bool b_pr
 // copied to the device; a device tensor is used as it is).
 at::Tensor gemm_a4w4_grouped(at::Tensor A, at::Tensor B, at::Tensor A_scale, at::Tensor B_scale,
                              at::Tensor group_offsets, c10::optional<at::Tensor> A_factor,
-                             c10::optional<at::Tensor> B_factor, int64_t config)
+                             c10::optional<at::Tensor> B_factor, int64_t config, double alpha,
+                             c10::optional<at::Tensor> bias)
 {
     TORCH_CHECK(group_offsets.dim() == 1 && group_offsets.numel() >= 2 &&
                     group_offsets.scalar_type() == at::kInt,
@@ -359,13 +360,20 @@ at::Tensor gemm_a4w4_grouped(at::Tensor A, at::Tensor B, at::Tensor A_scale, at:
         TORCH_CHECK(Af.is_cuda() && Bf.is_cuda() && Af.numel() == M && Bf.numel() == E * N,
                     "gemm_a4w4_grouped: factors must be device bytes of M and E*N entries");
     }
+    at::Tensor bz;
+    if (bias.has_value()) {
+        bz = bias->contiguous();
+        TORCH_CHECK(bz.is_cuda() && bz.device() == A.device() && bz.scalar_type() == at::kBFloat16 &&
+                        bz.numel() == E * N,
+                    "gemm_a4w4_grouped: bias must be a bf16 device tensor of E*N entries");
+    }
     auto out = torch::empty({Mpad, N}, torch::TensorOptions().dtype(torch::kBFloat16).device(A.device()));
-    check_status(mbs_gemm_a4w4_grouped_launch(
+    check_status(mbs_gemm_a4w4_grouped_launch_ex(
                      Au.data_ptr<uint8_t>(), Bu.data_ptr<uint8_t>(), Asu.data_ptr<uint8_t>(),
                      Bsu.data_ptr<uint8_t>(), Af.defined() ? Af.data_ptr<uint8_t>() : nullptr,
                      Bf.defined() ? Bf.data_ptr<uint8_t>() : nullptr, goff.data_ptr<int32_t>(), (int)E,
-                     out.data_ptr(), (int)M, (int)N, (int)K, (int)Mpad, (int)snp, (int)config,
-                     current_stream(A)),
+                     out.data_ptr(), (int)M, (int)N, (int)K, (int)Mpad, (int)snp, (float)alpha,
+                     bz.defined() ? bz.data_ptr() : nullptr, (int)config, current_stream(A)),
                  "gemm_a4w4_grouped");
     return out.narrow(0, 0, M);
 }
@@ -415,7 +423,8 @@ PYBIND11_MODULE(mbs_gemm_a4w4, m)
           pybind11::arg("A"), pybind11::arg("B"), pybind11::arg("A_scale"),
           pybind11::arg("B_scale"), pybind11::arg("group_offsets"),
           pybind11::arg("A_factor") = pybind11::none(), pybind11::arg("B_factor") = pybind11::none(),
-          pybind11::arg("config") = -1);
+          pybind11::arg("config") = -1, pybind11::arg("alpha") = 1.0,
+          pybind11::arg("bias") = pybind11::none());
     m.def("grouped_num_configs", []() { return mbs_gemm_a4w4_grouped_num_configs(); });
     m.def("grouped_config_name",
           [](int64_t c) { return std::string(mbs_gemm_a4w4_grouped_config_name((int)c)); });

@@ -3,7 +3,8 @@ experts against E separate dense launches on the same bytes (bit for bit:
 the per-element accumulation order does not depend on the tile), and against
 the oracle's run_torch per expert.  Covers every
 grouped configuration, empty experts, many small experts, MBS factors, a
-64-wide K tail, offsets given on the device, and the host-side checks."""
+64-wide K tail, offsets given on the device, alpha with a bias per expert,
+and the host-side checks."""
 import numpy as np
 import pytest
 
@@ -108,6 +109,44 @@ def test_grouped_default_plan(dev, rows, N, K, factors):
             xp[r0:r1], wq[e][0], xs[r0:r1], wq[e][1],
             None if af is None else af[r0:r1], None if bf is None else bf[e]))
         assert_close(bf16_to_f32(got[r0:r1]), ref, f"expert {e}")
+
+
+@pytest.mark.parametrize("config", [0, 1, 2, 3])
+def test_grouped_alpha_bias(dev, config):
+    """Affine epilogue per expert: bf16(C * alpha * f(a) * f(b) + bias[e]) --
+    the dense launch of each expert with its own bias row, bit for bit, and
+    the oracle's epilogue within tolerance."""
+    import torch
+
+    import mbs_amd
+
+    rows, N, K = [64, 0, 96, 32], 512, 1024
+    name = mbs_amd.ext().grouped_config_name(config)
+    say(f"grouped alpha/bias config={name} rows={rows} N={N} K={K}")
+    rng = np.random.default_rng(77 + config)
+    M, xp, xs, wq, af, bf, offs = make_problem(rng, rows, N, K, factors=True)
+    A, As, B, Bs, Af, Bf = device_operands(dev, M, N, K, xp, xs, wq, af, bf)
+    bias = oracle.f32_to_bf16_bits((rng.standard_normal((len(rows), N)) * 2).astype(np.float32))
+    bias_t = torch.from_numpy(bias.view(np.int16)).to(dev).view(torch.bfloat16)
+    got = mbs_amd.gemm_a4w4_grouped(A, B, As, Bs, torch.from_numpy(offs), Af, Bf, config=config,
+                                    alpha=-0.75, bias=bias_t)
+    torch.cuda.synchronize()
+    for e in range(len(rows)):
+        if rows[e] == 0:
+            continue
+        r0, r1 = offs[e], offs[e + 1]
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+        want = mbs_amd.gemm_a4w4(t(xp[r0:r1]), t(oracle.shuffle_b(wq[e][0])),
+                                 t(oracle.shuffle_scales(xs[r0:r1], K, pad=127)),
+                                 t(oracle.shuffle_scales(wq[e][1], K, pad=127)), t(af[r0:r1]), t(bf[e]),
+                                 alpha=-0.75, bias=bias_t[e])
+        assert torch.equal(got[r0:r1], want), (name, e)
+        c32 = (oracle.dequant_mxfp4(xp[r0:r1], xs[r0:r1]).astype(np.float64)
+               @ oracle.dequant_mxfp4(wq[e][0], wq[e][1]).astype(np.float64).T).astype(np.float32)
+        ref = oracle.bf16_bits_to_f32(oracle.epilogue_affine_bf16(c32, af[r0:r1], bf[e], -0.75, bias[e]))
+        assert_close(bf16_to_f32(got[r0:r1]), ref, f"{name} expert {e}")
+    with pytest.raises(RuntimeError, match="bias"):
+        mbs_amd.gemm_a4w4_grouped(A, B, As, Bs, torch.from_numpy(offs), bias=bias_t[0])
 
 
 def test_grouped_rejects_bad_offsets(dev):
