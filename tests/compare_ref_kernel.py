@@ -14,6 +14,13 @@ by HIP-graph replay (one graph of `copies` launches, replayed `replays`
 times).  Decode shapes rotate ten weight copies (cold: more bytes than the
 MALL); large shapes reuse one copy, as the reference's own measurement does
 (asm_vs_wg_kernel.md:179-180).  Prints one JSON object per shape.
+
+    python tests/compare_ref_kernel.py --only MxNxK --eager 4 [--own-configs a,b]
+
+launches each kernel 4 times eagerly (synchronised, untimed) instead: the
+form for hardware-counter runs (rocprofv3 --pmc ... -- python3 ...), which
+then see the reference's kernel, this library's plan and any named
+configurations on the same bytes.
 """
 from __future__ import annotations
 
@@ -59,6 +66,10 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--replays", type=int, default=20)
     ap.add_argument("--only", type=str, default="", help="comma list of MxNxK to run")
+    ap.add_argument("--eager", type=int, default=0, metavar="N",
+                    help="N synchronised eager launches of each kernel, no timing (counter runs)")
+    ap.add_argument("--own-configs", type=str, default="",
+                    help="with --eager: also launch these named configurations")
     args = ap.parse_args()
 
     import torch
@@ -127,6 +138,31 @@ def main():
         torch.cuda.synchronize()
         got, want = bf16_to_f32(out_own[:M]), bf16_to_f32(out_ref[:M])
         ratio = assert_close(got, want, "ours vs reference kernel")
+        if args.eager:
+            L.mbs_gemm_a4w4_config_name.restype = ctypes.c_char_p
+            names = [L.mbs_gemm_a4w4_config_name(i).decode() for i in range(L.mbs_gemm_a4w4_num_configs())]
+            for _ in range(args.eager):
+                launch_ref(0)
+                torch.cuda.synchronize()
+            for _ in range(args.eager):
+                launch_own(0)
+                torch.cuda.synchronize()
+            for nm in [c for c in args.own_configs.split(",") if c]:
+                c = names.index(nm)
+                wsc = L.mbs_gemm_a4w4_config_workspace_bytes(c, 1, M, N, K)
+                wst = torch.empty(max(wsc, 1), dtype=torch.uint8, device=dev)
+                for _ in range(args.eager):
+                    st = L.mbs_gemm_a4w4_launch_config(
+                        c, 1, P(A.data_ptr()), P(B.data_ptr()), P(As.data_ptr()), P(Bs.data_ptr()),
+                        pf(Af), pf(Bf), P(out_own.data_ptr()), M, N, K, Mpad, snp, P(wst.data_ptr()),
+                        wsc, P(torch.cuda.current_stream().cuda_stream))
+                    assert st == 0, L.mbs_last_error()
+                    torch.cuda.synchronize()
+            print(json.dumps({"shape": [M, N, K], "eager": args.eager, "factors": factors,
+                              "max_err_over_bound": round(ratio, 4)}), flush=True)
+            del A, B, As, Bs, Bc, Bsc, out_ref, out_own, ws
+            torch.cuda.empty_cache()
+            continue
 
         def graph_time(launch):
             torch.cuda.synchronize()
