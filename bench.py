@@ -215,8 +215,8 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures a single MI355X; the MXFP4 GEMM is a one-GPU "
-              "kernel here (multi-GPU sharding is described in DESIGN.md, not run). "
-              "Use --gpus 1.", file=sys.stderr)
+              "kernel here (a shard across GPUs is an ordinary (M, N/g, K) problem; no "
+              "multi-GPU run is part of it). Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
