@@ -87,7 +87,9 @@ int mbs_gemm_a4w4_launch_ex(int config, int splits, const uint8_t* A, const uint
  * group_offsets: device int32 [E+1], group_offsets[0] = 0, non-decreasing,
  * every entry a multiple of 32 (pad each expert's token block, as MoE
  * routing usually does), group_offsets[E] <= M; it is read by the kernel,
- * not checked on the host.  Rows past group_offsets[E] are not written.
+ * not checked on the host (offsets outside [0, M] are clamped into it on the
+ * device, so no store leaves the output).  Rows past group_offsets[E] are
+ * not written.
  * config: -1 for the heuristic, else 0 <= config <
  * mbs_gemm_a4w4_grouped_num_configs().  Each expert's rows give the same
  * bytes as mbs_gemm_a4w4_launch on that expert alone.  No counterpart in the

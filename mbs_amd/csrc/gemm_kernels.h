@@ -488,12 +488,19 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     // Grouped: the first M-tile index of each expert (prefix sums), in LDS.
     __shared__ int gtile[GROUPED ? kMaxGroups + 1 : 1];
     int tiles_m = p.tiles_m;
+    // Expert e's rows, clamped into [0, M]: the offsets come from the device
+    // and are not checked on the host, so no offset may move a store outside
+    // the output or raise the tile count past E * ceil(M / BM).
+    auto g_beg = [&](int e) __attribute__((always_inline)) { return min(max(p.groups[e], 0), p.M); };
+    auto g_end = [&](int e) __attribute__((always_inline)) {
+        return min(max(p.groups[e + 1], g_beg(e)), p.M);
+    };
     if constexpr (GROUPED) {
         if (threadIdx.x == 0) {
             int acc_t = 0;
             for (int e = 0; e < p.n_groups; ++e) {
                 gtile[e] = acc_t;
-                acc_t += (p.groups[e + 1] - p.groups[e] + T::BM - 1) / T::BM;
+                acc_t += (g_end(e) - g_beg(e) + T::BM - 1) / T::BM;
             }
             gtile[p.n_groups] = acc_t;
         }
@@ -534,9 +541,8 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                 else hi = mid - 1;
             }
             u.e = lo;
-            u.m0 = p.groups[lo] + (gm - gtile[lo]) * T::BM;
-            // offsets are not checked on the host: never store past row M
-            u.rowlim = min(p.groups[lo + 1], p.M);
+            u.m0 = g_beg(lo) + (gm - gtile[lo]) * T::BM;
+            u.rowlim = g_end(lo);   // rows past it are not stored
         } else {
             u.e = 0;
             u.m0 = gm * T::BM;
