@@ -131,12 +131,13 @@ const Config kConfigs[] = {
     {"bdirect_128x384_w1x4", kTiled, 128, 384, 256, 1, {0.455f, 0.455f, 4.55f}, launch_bdirect<B128x384w14>, true},
     // skinny: bm = rows covered (16*MT), bn = B rows per workgroup (16*NF)
     // eff = streaming efficiency relative to the best variant (cold N=K=8192 timings)
-    {"skinny_m16_n32_w16", kSkinny, 16, 32, 1024, 1, {0.95f, 0.f, 0.f}, launch_skinny<1, 2, 16, 4>},
-    {"skinny_m32_n32_w16", kSkinny, 32, 32, 1024, 1, {0.94f, 0.f, 0.f}, launch_skinny<2, 2, 16, 4>},
-    {"skinny_m16_n32_w8", kSkinny, 16, 32, 512, 2, {1.00f, 0.f, 0.f}, launch_skinny<1, 2, 8, 8>},
-    {"skinny_m32_n32_w8", kSkinny, 32, 32, 512, 2, {1.00f, 0.f, 0.f}, launch_skinny<2, 2, 8, 4>},
-    {"skinny_m16_n16_w8", kSkinny, 16, 16, 512, 2, {0.92f, 0.f, 0.f}, launch_skinny<1, 1, 8, 8>},
-    {"skinny_m32_n16_w8", kSkinny, 32, 16, 512, 2, {0.85f, 0.f, 0.f}, launch_skinny<2, 1, 8, 8>},
+    {"skinny_m16_n32_w16", kSkinny, 16, 32, 1024, 1, {0.94f, 0.f, 0.f}, launch_skinny<1, 2, 16, 4>},
+    {"skinny_m32_n32_w16", kSkinny, 32, 32, 1024, 1, {0.89f, 0.f, 0.f}, launch_skinny<2, 2, 16, 4>},
+    {"skinny_m16_n32_w8", kSkinny, 16, 32, 512, 2, {1.00f, 0.f, 0.f}, launch_skinny<1, 2, 8, 4>},
+    {"skinny_m32_n32_w8", kSkinny, 32, 32, 512, 2, {0.92f, 0.f, 0.f}, launch_skinny<2, 2, 8, 4>},
+    {"skinny_m16_n16_w8", kSkinny, 16, 16, 512, 2, {0.91f, 0.f, 0.f}, launch_skinny<1, 1, 8, 8>},
+    {"skinny_m32_n16_w8", kSkinny, 32, 16, 512, 2, {0.69f, 0.f, 0.f}, launch_skinny<2, 1, 8, 8>},
+    {"skinny_m32_n32_w4", kSkinny, 32, 32, 256, 2, {1.00f, 0.f, 0.f}, launch_skinny<2, 2, 4, 4>},
 };
 constexpr int kNumConfigs = (int)(sizeof(kConfigs) / sizeof(kConfigs[0]));
 constexpr int kNumCUs = 256;
@@ -164,6 +165,11 @@ void split_stages(int K, int want, int* sps, int* splits)
 
 double plan_cost(const Plan& pl, int M, int N, int K);
 
+// Streaming waves per CU a skinny configuration needs to reach its measured
+// rate: one workgroup per CU, at most 8 waves (timed cold at N=K=8192, the
+// 4-wave M=32 variant with one workgroup per CU was the fastest M=32 plan).
+int skinny_waves_per_cu(const Config& c) { return std::min(8, c.threads / 64); }
+
 bool make_plan(int config, int want_splits, int M, int N, int K, Plan* out)
 {
     if (config < 0 || config >= kNumConfigs) return false;
@@ -176,9 +182,10 @@ bool make_plan(int config, int want_splits, int M, int N, int K, Plan* out)
         const int nwk = c.threads / 64;
         int want = want_splits;
         if (want <= 0) {
-            // aim for ~8 resident streaming waves per CU, each with >= 2 stages
+            // aim for min(8, waves per workgroup) resident streaming waves per
+            // CU, each with >= 2 stages
             const int waves = wgs * nwk;
-            want = std::max(1, (kNumCUs * 8) / std::max(1, waves));
+            want = std::max(1, (kNumCUs * skinny_waves_per_cu(c)) / std::max(1, waves));
             want = std::min(want, std::max(1, stages_of(K) / (2 * nwk)));
         }
         split_stages(K, want, &pl.sps, &pl.splits);
@@ -231,10 +238,10 @@ double plan_cost(const Plan& pl, int M, int N, int K)
         ((double)M * K / 2 + (double)N * K / 2 + (double)(M + N) * K / 32 + 2.0 * M * N) /
         kHbmBytesPerNs;
     if (c.family == kSkinny) {
-        // bandwidth-bound: needs ~8 waves streaming B per CU to saturate HBM
+        // bandwidth-bound: needs skinny_waves_per_cu waves streaming B per CU
         const double wgs = (double)pl.grid.x * pl.grid.y;
         const double waves = wgs * (c.threads / 64);
-        const double occ = std::min(1.0, waves / (kNumCUs * 8.0));
+        const double occ = std::min(1.0, waves / (kNumCUs * (double)skinny_waves_per_cu(c)));
         const double a_ns = (double)pl.grid.x * c.bm * (K / 2) / kL2BytesPerNs;
         return kLaunchNs + hbm_ns / (std::max(occ, 0.02) * c.cost.a) + a_ns + split_ns;
     }

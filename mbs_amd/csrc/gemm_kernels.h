@@ -1217,6 +1217,15 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
     for (int st = my_begin; st < my_end; st += U) {
         i32x4 b[U][NF], a[U][MT];
         int sb[U / 2], sa[U / 2];
+        // Scales first: loads return in issue order, so stage u's MFMAs then
+        // wait only for stage u's B and A, and the MFMAs trail the stream
+        // instead of starting after the whole batch has landed.
+        static_for<U / 2>([&](auto v) {
+            const int g = (st >> 1) + v;
+            const bool ok = st + 2 * v < my_end;
+            sb[v] = load4(rBs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
+            sa[v] = load4(rAs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
+        });
         static_for<U>([&](auto u) {
             const int s = st + u;
             const bool ok = s < my_end;
@@ -1230,12 +1239,10 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
                                                       (lane >> 4) * 16));
             });
         });
-        static_for<U / 2>([&](auto v) {
-            const int g = (st >> 1) + v;
-            const bool ok = st + 2 * v < my_end;
-            sb[v] = load4(rBs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
-            sa[v] = load4(rAs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
-        });
+        // Every load of the batch is issued before the first MFMA; left to
+        // itself the scheduler interleaves them with the MFMAs and the wave
+        // keeps only a fraction of its batch in flight.
+        __builtin_amdgcn_sched_barrier(0);
         static_for<U>([&](auto u) {
             constexpr int h = u & 1;
             const int s = st + u;
@@ -1376,7 +1383,7 @@ using B128x256w14 = BdShape<128, 256, 1, 4>;
 #define MBS_BDIRECT_SHAPES_C(X) X(B256x256w14) X(B192x256w14) X(B96x256w14)
 #define MBS_BDIRECT_SHAPES_D(X) X(B64x512w14) X(B128x384w14) X(B128x256w14)
 #define MBS_GROUPED_SHAPES(X) X(B256x256) X(B128x256w14) X(B64x256) X(B64x128)
-#define MBS_SKINNY_SHAPES(X) X(1, 2, 16, 4) X(2, 2, 16, 4) X(1, 2, 8, 8) X(2, 2, 8, 4) X(1, 1, 8, 8) X(2, 1, 8, 8)
+#define MBS_SKINNY_SHAPES(X) X(1, 2, 16, 4) X(2, 2, 16, 4) X(1, 2, 8, 4) X(2, 2, 8, 4) X(1, 1, 8, 8) X(2, 1, 8, 8) X(2, 2, 4, 4)
 
 #define MBS_LAUNCH_SIG const GemmArgs&, dim3, bool, bool, hipStream_t
 #define MBS_TILED_INST(T) template hipError_t launch_tiled<T>(MBS_LAUNCH_SIG);
