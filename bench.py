@@ -199,6 +199,9 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip the decode shapes")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-grouped", action="store_true", help="skip the grouped (MoE) shapes")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only run the decode shapes (cold and warm graph replays) and print "
+                         "their block; for counter runs of the decode kernel")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 20 device-to-device copies of MIB MiB (scales the HBM "
                          "FETCH_SIZE/WRITE_SIZE counters) and exit")
@@ -224,6 +227,9 @@ def main():
     import mbs_amd
 
     dev = torch.device("cuda:0")
+    if args.decode_only:
+        print(json.dumps({"decode": decode_bench(dev)}), flush=True)
+        return
     M = N = K = 8192
     (A, B, As, Bs), (x, w) = prepare(M, N, K, 1, dev)
     step = lambda: mbs_amd.gemm_a4w4(A, B, As, Bs)
