@@ -21,8 +21,13 @@
  *                       f(b) = 1/(1+b/256).
  *   out      [Mpad, N]  bf16, Mpad = round_up(M,32); rows >= M untouched.
  *   scaleN_pad = round_up(ceil(K/32), 8).
- * Requirements: M >= 1, N % 16 == 0, K % 64 == 0 (the (16,16) preshuffle
- * needs K/2 % 32 == 0), all pointers device-accessible.
+ * Requirements: M >= 0, N % 16 == 0, K % 64 == 0 (the (16,16) preshuffle
+ * needs K/2 % 32 == 0), all pointers device-accessible.  M == 0 (an empty
+ * batch, e.g. an expert without tokens) validates the other arguments and
+ * returns MBS_OK without launching; A, its scales and factors and out may
+ * then be NULL.  The reference's launcher also reports success there
+ * (kernel/gemm_a4w4.hip:1044-1146 launches a zero-size grid and does not
+ * check the launch status).
  *
  * Every launch is asynchronous on `stream`; results are deterministic
  * (split-K partials are reduced in a fixed order, no atomics).

@@ -338,11 +338,14 @@ int validate(const uint8_t* A, const uint8_t* B, const uint8_t* As, const uint8_
              const uint8_t* Af, const uint8_t* Bf, void* out, int M, int N, int K, int Mpad,
              int snp)
 {
-    if (!A || !B || !As || !Bs || !out) return fail(MBS_ERR_ARGUMENT, "null operand pointer");
-    if ((Af == nullptr) != (Bf == nullptr))
+    // M == 0 (an empty batch) is valid: A, its scales, its factors and out
+    // may then be the null data pointers of empty tensors.
+    if (!B || !Bs || (M > 0 && (!A || !As || !out)))
+        return fail(MBS_ERR_ARGUMENT, "null operand pointer");
+    if ((Af == nullptr) != (Bf == nullptr) && M > 0)
         return fail(MBS_ERR_ARGUMENT, "AFactor and BFactor must be given together");
-    if (M < 1 || N < 16 || K < 64)
-        return fail(MBS_ERR_ARGUMENT, "need M >= 1, N >= 16, K >= 64; got M=" + std::to_string(M) +
+    if (M < 0 || N < 16 || K < 64)
+        return fail(MBS_ERR_ARGUMENT, "need M >= 0, N >= 16, K >= 64; got M=" + std::to_string(M) +
                                           " N=" + std::to_string(N) + " K=" + std::to_string(K));
     if (N % 16) return fail(MBS_ERR_ARGUMENT, "N must be a multiple of 16, got " + std::to_string(N));
     if (K % 64)
@@ -505,7 +508,7 @@ int mbs_gemm_a4w4_launch(const uint8_t* A, const uint8_t* B, const uint8_t* ASca
 {
     set_last_error("");
     int st = validate(A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, Mpad, scaleN_pad);
-    if (st != MBS_OK) return st;
+    if (st != MBS_OK || M == 0) return st;
     Plan pl;
     if (!choose_plan(M, N, K, workspace ? workspace_bytes : 0, &pl))
         return fail(MBS_ERR_CONFIG, "no kernel configuration fits this problem");
@@ -544,6 +547,7 @@ int mbs_gemm_a4w4_grouped_launch_ex(const uint8_t* A, const uint8_t* B, const ui
     if (config < -1 || config >= kNumGrouped)
         return fail(MBS_ERR_CONFIG, "grouped config out of range");
     if (!(alpha == alpha)) return fail(MBS_ERR_ARGUMENT, "alpha is NaN");
+    if (M == 0) return MBS_OK;
     const int g = config >= 0 ? config : choose_grouped(M, N, K, num_groups);
     return run_grouped(g, A, B, AScale, BScale, AFactor, BFactor, group_offsets, num_groups, out, M,
                        N, K, scaleN_pad, stream, alpha, bias);
@@ -590,6 +594,9 @@ int mbs_gemm_a4w4_launch_config(int config, int splits, const uint8_t* A, const 
     set_last_error("");
     int st = validate(A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, Mpad, scaleN_pad);
     if (st != MBS_OK) return st;
+    if (config < 0 || config >= kNumConfigs)
+        return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) + " out of range");
+    if (M == 0) return MBS_OK;
     Plan pl;
     if (!make_plan(config, splits, M, N, K, &pl))
         return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) + " cannot run M=" +
@@ -608,6 +615,9 @@ int mbs_gemm_a4w4_launch_ex(int config, int splits, const uint8_t* A, const uint
     int st = validate(A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, Mpad, scaleN_pad);
     if (st != MBS_OK) return st;
     if (!(alpha == alpha)) return fail(MBS_ERR_ARGUMENT, "alpha is NaN");
+    if (config >= kNumConfigs)
+        return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) + " out of range");
+    if (M == 0) return MBS_OK;
     Plan pl;
     if (config < 0) {
         if (!choose_plan(M, N, K, workspace ? workspace_bytes : 0, &pl))

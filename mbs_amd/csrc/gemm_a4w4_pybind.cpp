@@ -67,7 +67,6 @@ Operands prepare(const at::Tensor& A, const at::Tensor& B, const at::Tensor& A_s
     o.N = (int)o.B.size(0);
     TORCH_CHECK(o.B.size(1) == Kp, "gemm_a4w4: A, B must share K/2, got ", o.A.size(1), " vs ",
                 o.B.size(1));
-    TORCH_CHECK(o.M >= 1, "gemm_a4w4: M must be >= 1");
     TORCH_CHECK(o.K % 32 == 0, "gemm_a4w4: K must be a multiple of 32, got ", o.K);
     TORCH_CHECK(o.K % 64 == 0, "gemm_a4w4: K must be a multiple of 64 (the (16,16) B preshuffle "
                 "groups 32 bytes of K), got ", o.K);

@@ -35,6 +35,8 @@ def c_lib():
     P, I, S = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
     L.mbs_gemm_a4w4_launch.argtypes = [P, P, P, P, P, P, P, I, I, I, I, I, P, S, P]
     L.mbs_gemm_a4w4_launch.restype = I
+    L.mbs_gemm_a4w4_launch_config.argtypes = [I, I, P, P, P, P, P, P, P, I, I, I, I, I, P, S, P]
+    L.mbs_gemm_a4w4_launch_config.restype = I
     L.mbs_status_string.restype = ctypes.c_char_p
     L.mbs_last_error.restype = ctypes.c_char_p
     L.mbs_gemm_a4w4_plan_name.argtypes = [I, I, I, ctypes.c_char_p, S]
@@ -44,11 +46,12 @@ def c_lib():
     return L
 
 
-FAKE = 0x1000  # never dereferenced: validation fails first
+FAKE = 0x1000  # never dereferenced: validation fails first (or M == 0 returns early)
 
 
 @pytest.mark.parametrize("M,N,K,Mpad,snp,why", [
-    (0, 256, 512, 32, 16, "M >= 1"),
+    (-1, 256, 512, 0, 16, "M >= 0"),
+    (0, 256, 512, 32, 16, "Mpad"),
     (128, 250, 512, 128, 16, "multiple of 16"),
     (128, 256, 480, 128, 16, "multiple of 64"),
     (128, 256, 512, 130, 16, "Mpad"),
@@ -61,6 +64,26 @@ def test_launch_rejects_bad_shapes(M, N, K, Mpad, snp, why):
     assert st == 1  # MBS_ERR_ARGUMENT
     assert why in L.mbs_last_error().decode()
     assert L.mbs_status_string(st) == b"invalid argument"
+
+
+def test_empty_batch_is_a_validated_no_op():
+    """M == 0: success without a launch (no GPU call is made), null A / out allowed;
+    the other arguments are still checked."""
+    L = c_lib()
+    assert L.mbs_gemm_a4w4_launch(None, FAKE, None, FAKE, None, None, None, 0, 256, 512, 0, 16,
+                                  None, 0, None) == 0
+    assert L.mbs_gemm_a4w4_launch_config(0, 1, None, FAKE, None, FAKE, None, FAKE, None, 0, 256,
+                                         512, 0, 16, None, 0, None) == 0
+    # still validated: N, K, Mpad, B pointers and the config index
+    assert L.mbs_gemm_a4w4_launch(None, FAKE, None, FAKE, None, None, None, 0, 250, 512, 0, 16,
+                                  None, 0, None) == 1
+    assert L.mbs_gemm_a4w4_launch(None, None, None, FAKE, None, None, None, 0, 256, 512, 0, 16,
+                                  None, 0, None) == 1
+    assert L.mbs_gemm_a4w4_launch_config(10**6, 1, None, FAKE, None, FAKE, None, None, None, 0,
+                                         256, 512, 0, 16, None, 0, None) == 4
+    # M > 0 still needs A and out
+    assert L.mbs_gemm_a4w4_launch(None, FAKE, FAKE, FAKE, None, None, FAKE, 32, 256, 512, 32, 16,
+                                  None, 0, None) == 1
 
 
 def test_launch_rejects_null_and_half_factors():

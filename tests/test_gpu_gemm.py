@@ -199,3 +199,27 @@ def test_pybind_module_matches_c_abi(dev, gold):
         m.gemm_a4w4(c.A, c.B, c.As, c.Bs, c.Af, None)
     with pytest.raises(RuntimeError, match="A_scale must hold"):
         m.gemm_a4w4(c.A, c.B, c.As[:10], c.Bs)
+
+
+def test_empty_batch(dev, gold):
+    """M == 0 (an expert without tokens): the module returns an empty [0, N]
+    bf16 tensor and launches nothing, with and without factors, for the default
+    plan and a forced configuration; the next call still computes normally."""
+    import torch
+
+    import mbs_amd
+
+    m = mbs_amd.ext()
+    c = Case(gold["x_packed"], gold["x_scales"], gold["w_packed"], gold["w_scales"])
+    say("empty batch M=0")
+    A0 = c.A[:0]
+    As0 = torch.empty(0, dtype=torch.uint8, device=c.A.device)
+    Af0 = torch.empty(0, dtype=torch.uint8, device=c.A.device)
+    Bf = torch.zeros(c.N, dtype=torch.uint8, device=c.A.device)
+    for out in (m.gemm_a4w4(A0, c.B, As0, c.Bs), m.gemm_a4w4(A0, c.B, As0, c.Bs, Af0, Bf),
+                m.gemm_a4w4_config(0, 1, A0, c.B, As0, c.Bs),
+                m.gemm_a4w4(A0, c.B, As0, c.Bs, alpha=2.0)):
+        assert out.shape == (0, c.N) and out.dtype == torch.bfloat16 and out.is_cuda
+    torch.cuda.synchronize()
+    assert_close(bf16_to_f32(m.gemm_a4w4(c.A, c.B, c.As, c.Bs)),
+                 oracle.bf16_bits_to_f32(gold["c_bf16"]), "call after the empty batch")
