@@ -13,8 +13,9 @@ Also reported (same JSON line): the decode shapes of configs[2]
 (M in {1,4,16,32}, N=K=8192) measured cold -- ten rotating weight copies,
 more than the 256 MB MALL -- replayed from a HIP graph; and the CPU baseline
 (the oracle's restatement of the reference's run_torch on this host's cores,
-on a bounded sample); and the grouped (mixture-of-experts) GEMM on
-configs[3]'s expert shapes, one launch against one dense launch per expert.
+on a bounded sample); the grouped (mixture-of-experts) GEMM on
+configs[3]'s expert shapes, one launch against one dense launch per expert;
+and the activation quantizer (bf16 -> MXFP4) against HBM bandwidth.
 
 One GPU only: --gpus above 1 exits with an explanation.
 """
@@ -110,6 +111,47 @@ def decode_bench(dev, Ms=(1, 4, 16, 32), N=8192, K=8192, copies=10, replays=20):
     return res
 
 
+def quantize_bench(dev, shapes=((8192, 8192), (2048, 7168), (32, 8192)), replays=5, reps=3):
+    """The activation quantizer (bf16 -> packed e2m1 + shuffled E8M0, the
+    reference's aiter per_1x32 step) on configs[1]'s A, configs[3]'s
+    M=2048 x K=7168 A and a decode-sized A: HIP-graph replays of 10 calls,
+    HBM bytes = 2*R*K read + R*K/2 + R*K/32 written, against 8 TB/s."""
+    import torch
+
+    import mbs_amd
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(1005)
+    res = {}
+    for R, K in shapes:
+        x = torch.randn(R, K, generator=g, device=dev).to(torch.bfloat16)
+        call = lambda: mbs_amd.quantize_mxfp4(x, shuffle=True)
+        call()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(10):
+                call()
+        gr.replay()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(replays):
+                gr.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3 / (replays * 10))
+        us = statistics.median(ts)
+        nbytes = 2 * R * K + R * K // 2 + R * K // 32
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[f"{R}x{K}"] = {"us": round(us, 2), "GBps": round(gbs, 1),
+                           "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+        del gr, x
+    return res
+
+
 def grouped_bench(dev, experts=8, rows=256, shapes=((7168, 2048), (4096, 7168), (2112, 7168)),
                   replays=10):
     """Grouped GEMM over `experts` experts of `rows` tokens each (configs[3]'s
@@ -199,6 +241,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip the decode shapes")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-grouped", action="store_true", help="skip the grouped (MoE) shapes")
+    ap.add_argument("--no-quantize", action="store_true", help="skip the activation quantizer")
     ap.add_argument("--decode-only", action="store_true",
                     help="only run the decode shapes (cold and warm graph replays) and print "
                          "their block; for counter runs of the decode kernel")
@@ -263,6 +306,8 @@ def main():
     del A, B, As, Bs
     if not args.no_grouped:
         line["grouped"] = grouped_bench(dev)
+    if not args.no_quantize:
+        line["quantize"] = quantize_bench(dev)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(x, w)
     print(json.dumps(line), flush=True)

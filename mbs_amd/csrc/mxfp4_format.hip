@@ -9,6 +9,8 @@
 
 namespace mbs {
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ int64_t flat_b(int64_t n, int64_t kp, int64_t Kp)
 {
     return (n >> 4) * (Kp * 16) + (kp >> 5) * 512 + ((kp & 31) >> 4) * 256 + (n & 15) * 16 +
@@ -29,12 +31,42 @@ __device__ __forceinline__ int floor_log2_bits(uint32_t u)
     return (31 - __builtin_clz(u & 0x7FFFFFu)) - 149;
 }
 
+// E8M0 scale of a block from its largest magnitude (fp32 bits, already times
+// the row multiplier m) and its NaN flag: floor(log2(amax)) - 2, biased by
+// 127 and clamped to [0, 254]; 0 for an all-zero block, 254 for an infinite
+// maximum, 255 (NaN) when the block holds a NaN.
+__device__ __forceinline__ uint32_t e8m0_of(uint32_t amax_m, bool nan)
+{
+    if (nan) return 255;
+    if (amax_m == 0) return 0;
+    if (amax_m >= 0x7F800000u) return 254;
+    const int e = floor_log2_bits(amax_m) - 2 + 127;
+    return (uint32_t)(e < 0 ? 0 : (e > 254 ? 254 : e));
+}
+
+// 2^(s - 127) for s in [0, 254] as fp32: exponent field s, or the subnormal
+// 2^-127 for s == 0.
+__device__ __forceinline__ float e8m0_value(uint32_t s)
+{
+    return s == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(s << 23);
+}
+
+// The e2m1 codes of the block are produced by the gfx950 scaled conversions
+// v_cvt_scalef32_pk_fp4_{f32,bf16}: code = RNE(v / scale) on the e2m1 grid
+// {0, .5, 1, 1.5, 2, 3, 4, 6} with ties to the even code and saturation at
+// 6, sign kept (so -0 and negative values that round to zero give code 8);
+// the first source goes to the low nibble, and the last argument selects the
+// destination byte.  These semantics were measured on MI355X against the
+// oracle's rule for every multiple of 1/8 in [-9, 9] (all ties), +-0, +-inf,
+// huge and subnormal values, under scales 2^-127 .. 2^127; only NaN differs
+// (the hardware gives code 7), and NaN blocks are written as zeros here, as
+// the oracle does.  With scale = 2^(s-127) this is the oracle's
+// q = x * 2^(127-s) followed by its midpoint count.
+
 // Quantize one 32-element K-block (bf16 words w, two values each) scaled by
 // m: amax -> E8M0, then e2m1 round to nearest even on the code with
-// saturation at 6.  The code of |q| is the number of grid midpoints it
-// passes: ties at 0.25, 1.25, 2.5, 5 go down to the even code, ties at 0.75,
-// 1.75, 3.5 go up to it.  m is 1 or an MBS row multiplier 1 + b/256; every
-// product is exact in fp32 (8 + 9 significant bits) and positive scaling is
+// saturation at 6.  m is 1 or an MBS row multiplier 1 + b/256; every product
+// x*m is exact in fp32 (8 + 9 significant bits) and positive scaling is
 // monotone, so the block maximum is the bf16 maximum times m.
 __device__ __forceinline__ void quantize_block(const uint32_t w[16], float m, uint32_t out[4],
                                                uint32_t* scale)
@@ -49,28 +81,18 @@ __device__ __forceinline__ void quantize_block(const uint32_t w[16], float m, ui
         nan |= mg > 0x7F800000u;
         amax_bits = (mg > amax_bits && mg <= 0x7F800000u) ? mg : amax_bits;
     }
-    const uint32_t amax_m = __float_as_uint(__uint_as_float(amax_bits) * m);
-    uint32_t s;
-    if (nan) s = 255;
-    else if (amax_m == 0) s = 0;
-    else if (amax_m >= 0x7F800000u) s = 254;
-    else {
-        int e = floor_log2_bits(amax_m) - 2 + 127;
-        s = (uint32_t)(e < 0 ? 0 : (e > 254 ? 254 : e));
-    }
-    // 2^(127 - s), s in [0, 254]: exponent field 254 - s, or the subnormal
-    // 2^-127 for s == 254.
-    const float inv = (s == 254) ? __uint_as_float(0x00400000u) : __uint_as_float((254u - s) << 23);
-    for (int i = 0; i < 4; ++i) out[i] = 0;
-    for (int i = 0; i < 32; ++i) {
-        const uint32_t h = (i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xFFFF);
-        const float q = (__uint_as_float((h & 0x7FFF) << 16) * m) * inv;
-        uint32_t c = (uint32_t)(q > 0.25f) + (uint32_t)(q >= 0.75f) + (uint32_t)(q > 1.25f) +
-                     (uint32_t)(q >= 1.75f) + (uint32_t)(q > 2.5f) + (uint32_t)(q >= 3.5f) +
-                     (uint32_t)(q > 5.0f);
-        c |= (h >> 12) & 8u;  // sign
-        if (nan) c = 0;
-        out[i >> 3] |= c << (4 * (i & 7));
+    const uint32_t s = e8m0_of(__float_as_uint(__uint_as_float(amax_bits) * m), nan);
+    const float sc = e8m0_value(s == 255 ? 127 : s);
+    for (int i = 0; i < 4; ++i) {
+        uint32_t o = 0;
+        static_for<4>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            const uint32_t wv = w[4 * i + j];
+            const float lo = __uint_as_float(wv << 16) * m;
+            const float hi = __uint_as_float(wv & 0xFFFF0000u) * m;
+            o = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(o, lo, hi, sc, j);
+        });
+        out[i] = nan ? 0u : o;
     }
     *scale = s;
 }
@@ -99,19 +121,48 @@ __device__ __forceinline__ void store_block(int r, int b, int K, int nb, int snp
     if (sshuf) sshuf[flat_s(r, b, snp)] = (uint8_t)s;
 }
 
-// One thread per 32-element K-block.
+// Plain quantization, four lanes per 32-element K-block: lane q of a quad
+// loads elements 8q..8q+7 (16 bytes, so a wave reads 1 KiB of a row
+// contiguously), the quad combines its magnitudes into the block maximum, and
+// each lane converts its 8 elements into one dword of packed output
+// (v_cvt_scalef32_pk_fp4_bf16 straight from the bf16 pairs).  blockIdx.x:
+// group of 4 rows (threadIdx.y), blockIdx.y: group of 64 chunks.
 __global__ void __launch_bounds__(256)
 quantize_bf16_kernel(const uint16_t* __restrict__ x, int rows, int K, uint8_t* __restrict__ packed,
                      uint8_t* __restrict__ sshuf, uint8_t* __restrict__ splain, int snp)
 {
-    const int nb = K >> 5;
-    const int64_t blk = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (blk >= (int64_t)rows * nb) return;
-    const int r = (int)(blk / nb), b = (int)(blk - (int64_t)r * nb);
-    uint32_t w[16], out[4], s;
-    load_block(x + (int64_t)r * K + b * 32, w);
-    quantize_block(w, 1.0f, out, &s);
-    store_block(r, b, K, nb, snp, out, s, packed, sshuf, splain);
+    const int nc = K >> 3;                               // 16-byte chunks per row
+    const int j = blockIdx.y * 64 + threadIdx.x;          // chunk in the row
+    const int r = blockIdx.x * 4 + threadIdx.y;           // row (uniform per wave)
+    // nc % 4 == 0 and quads are 4-aligned: whole quads leave together, so
+    // the quad exchanges below only read active lanes.
+    if (r >= rows || j >= nc) return;
+    const i32x4 v = *reinterpret_cast<const i32x4*>(x + (int64_t)r * K + (int64_t)j * 8);
+    // magnitude maximum on the 15 magnitude bits: a NaN orders above inf
+    uint32_t mx = 0;
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t w = (uint32_t)v[i] & 0x7FFF7FFFu;
+        mx = max(mx, max(w & 0xFFFFu, w >> 16));
+    }
+    mx = max(mx, (uint32_t)__shfl_xor((int)mx, 1));
+    mx = max(mx, (uint32_t)__shfl_xor((int)mx, 2));
+    const bool nan = mx > 0x7F80u;
+    const uint32_t s = e8m0_of(mx << 16, nan);
+    const float sc = e8m0_value(nan ? 127 : s);
+    // (each word is copied to a scalar first: hipcc's __builtin_bit_cast of a
+    // vector element v[i] reads element 0)
+    const uint32_t w0 = (uint32_t)v[0], w1 = (uint32_t)v[1], w2 = (uint32_t)v[2], w3 = (uint32_t)v[3];
+    uint32_t o = 0;
+    o = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(o, __builtin_bit_cast(bf16x2_t, w0), sc, 0);
+    o = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(o, __builtin_bit_cast(bf16x2_t, w1), sc, 1);
+    o = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(o, __builtin_bit_cast(bf16x2_t, w2), sc, 2);
+    o = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(o, __builtin_bit_cast(bf16x2_t, w3), sc, 3);
+    *reinterpret_cast<uint32_t*>(packed + (int64_t)r * (K >> 1) + (int64_t)j * 4) = nan ? 0u : o;
+    if ((threadIdx.x & 3) == 0) {
+        const int b = j >> 2;
+        if (splain) splain[(int64_t)r * (K >> 5) + b] = (uint8_t)s;
+        if (sshuf) sshuf[flat_s(r, b, snp)] = (uint8_t)s;
+    }
 }
 
 // MBS quantization (docs/kernel_advanced.md:120-129 of the reference): one
@@ -326,6 +377,7 @@ int mbs_quantize_mxfp4_bf16(const void* x, int rows, int K, uint8_t* packed,
 {
     if (!x || !packed) return fmt_fail("null pointer");
     if (rows < 1 || K < 32 || K % 32) return fmt_fail("need rows >= 1 and K % 32 == 0");
+    if (K / 512 >= 65535) return fmt_fail("K too large for the quantizer grid");
     if (pad_byte < 0 || pad_byte > 255) return fmt_fail("pad_byte must be a byte");
     (void)hipGetLastError();
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -337,8 +389,8 @@ int mbs_quantize_mxfp4_bf16(const void* x, int rows, int K, uint8_t* packed,
             hipLaunchKernelGGL(scale_pad_kernel, dim3(blocks_for(n)), dim3(256), 0, s,
                                scale_shuffled, rows, nb, snp, (uint8_t)pad_byte);
     }
-    hipLaunchKernelGGL(quantize_bf16_kernel, dim3(blocks_for((int64_t)rows * nb)), dim3(256), 0,
-                       s, static_cast<const uint16_t*>(x), rows, K, packed, scale_shuffled,
+    hipLaunchKernelGGL(quantize_bf16_kernel, dim3((rows + 3) / 4, (K / 8 + 63) / 64), dim3(64, 4),
+                       0, s, static_cast<const uint16_t*>(x), rows, K, packed, scale_shuffled,
                        scale_plain, snp);
     return launched();
 }
