@@ -63,64 +63,6 @@ __device__ __forceinline__ float e8m0_value(uint32_t s)
 // the oracle does.  With scale = 2^(s-127) this is the oracle's
 // q = x * 2^(127-s) followed by its midpoint count.
 
-// Quantize one 32-element K-block (bf16 words w, two values each) scaled by
-// m: amax -> E8M0, then e2m1 round to nearest even on the code with
-// saturation at 6.  m is 1 or an MBS row multiplier 1 + b/256; every product
-// x*m is exact in fp32 (8 + 9 significant bits) and positive scaling is
-// monotone, so the block maximum is the bf16 maximum times m.
-__device__ __forceinline__ void quantize_block(const uint32_t w[16], float m, uint32_t out[4],
-                                               uint32_t* scale)
-{
-    // bf16 -> fp32 bits is a 16-bit shift; track amax on the magnitude bits
-    // (monotone for non-NaN values) and NaN separately.
-    uint32_t amax_bits = 0;
-    bool nan = false;
-    for (int i = 0; i < 32; ++i) {
-        const uint32_t h = (i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xFFFF);
-        const uint32_t mg = (h & 0x7FFF) << 16;
-        nan |= mg > 0x7F800000u;
-        amax_bits = (mg > amax_bits && mg <= 0x7F800000u) ? mg : amax_bits;
-    }
-    const uint32_t s = e8m0_of(__float_as_uint(__uint_as_float(amax_bits) * m), nan);
-    const float sc = e8m0_value(s == 255 ? 127 : s);
-    for (int i = 0; i < 4; ++i) {
-        uint32_t o = 0;
-        static_for<4>([&](auto J) {
-            constexpr int j = decltype(J)::value;
-            const uint32_t wv = w[4 * i + j];
-            const float lo = __uint_as_float(wv << 16) * m;
-            const float hi = __uint_as_float(wv & 0xFFFF0000u) * m;
-            o = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(o, lo, hi, sc, j);
-        });
-        out[i] = nan ? 0u : o;
-    }
-    *scale = s;
-}
-
-__device__ __forceinline__ void load_block(const uint16_t* p, uint32_t w[16])
-{
-    const i32x4* src = reinterpret_cast<const i32x4*>(p);
-    for (int i = 0; i < 4; ++i) {
-        const i32x4 v = src[i];
-        w[4 * i + 0] = v[0];
-        w[4 * i + 1] = v[1];
-        w[4 * i + 2] = v[2];
-        w[4 * i + 3] = v[3];
-    }
-}
-
-__device__ __forceinline__ void store_block(int r, int b, int K, int nb, int snp,
-                                            const uint32_t out[4], uint32_t s,
-                                            uint8_t* __restrict__ packed,
-                                            uint8_t* __restrict__ sshuf,
-                                            uint8_t* __restrict__ splain)
-{
-    i32x4 o = {(int)out[0], (int)out[1], (int)out[2], (int)out[3]};
-    *reinterpret_cast<i32x4*>(packed + (int64_t)r * (K >> 1) + b * 16) = o;
-    if (splain) splain[(int64_t)r * nb + b] = (uint8_t)s;
-    if (sshuf) sshuf[flat_s(r, b, snp)] = (uint8_t)s;
-}
-
 // Plain quantization, four lanes per 32-element K-block: lane q of a quad
 // loads elements 8q..8q+7 (16 bytes, so a wave reads 1 KiB of a row
 // contiguously), the quad combines its magnitudes into the block maximum, and
@@ -203,12 +145,37 @@ quantize_mbs_bf16_kernel(const uint16_t* __restrict__ x, int K, uint8_t* __restr
     }
     const float m = __uint_as_float(0x3F800000u | (fb << 15));
     if (threadIdx.x == 0) factors[r] = (uint8_t)fb;
+    // Quantize pass, four lanes per 32-element block as in the plain kernel:
+    // quad k of the workgroup takes blocks k, k + 64, ...; lane q of the quad
+    // elements 8q..8q+7 of the block.  nb blocks per row: whole quads take
+    // part in an iteration or none does, so the quad exchanges read active lanes.
     const int nb = K >> 5;
-    for (int b = threadIdx.x; b < nb; b += 256) {
-        uint32_t w[16], out[4], s;
-        load_block(xr + b * 32, w);
-        quantize_block(w, m, out, &s);
-        store_block(r, b, K, nb, snp, out, s, packed, sshuf, splain);
+    const int q = threadIdx.x & 3;
+    for (int b = threadIdx.x >> 2; b < nb; b += 64) {
+        const i32x4 v = *reinterpret_cast<const i32x4*>(xr + b * 32 + q * 8);
+        const uint32_t w[4] = {(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+        uint32_t mx = 0;
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t a = w[i] & 0x7FFF7FFFu;
+            mx = max(mx, max(a & 0xFFFFu, a >> 16));
+        }
+        mx = max(mx, (uint32_t)__shfl_xor((int)mx, 1));
+        mx = max(mx, (uint32_t)__shfl_xor((int)mx, 2));
+        const bool nan = mx > 0x7F80u;
+        const uint32_t s = e8m0_of(__float_as_uint(__uint_as_float(mx << 16) * m), nan);
+        const float sc = e8m0_value(nan ? 127 : s);
+        uint32_t o = 0;
+        static_for<4>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            const float lo = __uint_as_float(w[j] << 16) * m;
+            const float hi = __uint_as_float(w[j] & 0xFFFF0000u) * m;
+            o = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(o, lo, hi, sc, j);
+        });
+        *reinterpret_cast<uint32_t*>(packed + (int64_t)r * (K >> 1) + b * 16 + q * 4) = nan ? 0u : o;
+        if (q == 0) {
+            if (splain) splain[(int64_t)r * nb + b] = (uint8_t)s;
+            if (sshuf) sshuf[flat_s(r, b, snp)] = (uint8_t)s;
+        }
     }
 }
 
