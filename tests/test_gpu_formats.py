@@ -61,6 +61,41 @@ def test_quantize_bit_exact(dev, R, K):
     np.testing.assert_array_equal(host(shuf), ref_shuf)
 
 
+@pytest.mark.parametrize("R,K", [(5, 4128), (7, 96), (4, 32)])
+def test_quantize_special_values_and_ragged_grids(dev, R, K):
+    """NaN, +-inf, -0, negative values that round to zero and extreme mixes in one
+    block, on row counts that are not a multiple of the kernel's 4-row groups and
+    chunk counts that leave a partial 64-chunk group (K = 4128: 516 chunks)."""
+    import torch
+
+    rng = np.random.default_rng(R + K)
+    bits = rng.integers(0, 2**16, (R, K), dtype=np.uint32).astype(np.uint16)
+    bits[0, 3] = 0x7FC1                    # NaN: scale 255, block codes 0
+    bits[0, 40 % K] = 0xFF80                # -inf (block saturates unless it holds the NaN)
+    bits[1, :32] = 0x8000                   # -0 block
+    bits[1, 32 % K:(32 % K) + 2] = 0x7F80   # +inf
+    bits[2, :32] = 0x8001                   # negative subnormals
+    bits[2, 5] = 0x7F7F                     # next to the largest finite value
+    if R > 3:
+        bits[3, :16] = 0x0001               # tiny positive with a huge one in the block
+        bits[3, 16] = 0x7F00
+    xf = (bits.astype(np.uint32) << 16).view(np.float32)
+    ref_p, ref_s = oracle.quantize_mxfp4(xf)
+    ref_shuf = oracle.shuffle_scales(ref_s, K, pad=0x33)
+    L = clib()
+    x = to_dev(bits)
+    packed = torch.empty(R, K // 2, dtype=torch.uint8, device=dev)
+    shuf = torch.full(ref_shuf.shape, 0, dtype=torch.uint8, device=dev)
+    plain = torch.empty(R, K // 32, dtype=torch.uint8, device=dev)
+    say(f"quantize specials R={R} K={K}")
+    assert L.mbs_quantize_mxfp4_bf16(ptr(x), R, K, ptr(packed), ptr(shuf), ptr(plain), 0x33,
+                                     stream_ptr()) == 0
+    np.testing.assert_array_equal(host(packed), ref_p)
+    np.testing.assert_array_equal(host(plain), ref_s)
+    np.testing.assert_array_equal(host(shuf), ref_shuf)
+    assert ref_s[0, 0] == 255 and (K == 32 or ref_s[1, 0] == 0)
+
+
 @pytest.mark.parametrize("N,K", [(16, 64), (48, 512), (256, 2048)])
 def test_shuffles_bit_exact(dev, N, K):
     import torch
