@@ -22,7 +22,9 @@
  *   out      [Mpad, N]  bf16, Mpad = round_up(M,32); rows >= M untouched.
  *   scaleN_pad = round_up(ceil(K/32), 8).
  * Requirements: M >= 0, N % 16 == 0, K % 64 == 0 (the (16,16) preshuffle
- * needs K/2 % 32 == 0), all pointers device-accessible.  M == 0 (an empty
+ * needs K/2 % 32 == 0), all pointers device-accessible.  Size limits (32-bit
+ * buffer offsets): M*K/2 and N*K/2 below 2^31 bytes, 256*N*4 below 2^31; the
+ * output itself may exceed 2^31 bytes (it is addressed per tile).  M == 0 (an empty
  * batch, e.g. an expert without tokens) validates the other arguments and
  * returns MBS_OK without launching; A, its scales and factors and out may
  * then be NULL.  The reference's launcher also reports success there

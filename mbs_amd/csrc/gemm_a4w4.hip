@@ -355,9 +355,13 @@ int validate(const uint8_t* A, const uint8_t* B, const uint8_t* As, const uint8_
         return fail(MBS_ERR_ARGUMENT, "Mpad must be round_up(M, 32)");
     if (snp != ((K + 31) / 32 + 7) / 8 * 8)
         return fail(MBS_ERR_ARGUMENT, "scaleN_pad must be round_up(ceil(K/32), 8)");
+    // 32-bit buffer offsets: A and B are each one resource; the output and the
+    // split-K workspace are addressed per tile (64-bit tile base, at most 256
+    // rows below it), except in the decode kernel (M <= 32), which spans the
+    // whole [M, N] output with one resource.
     if ((int64_t)512 * (K / 2) + 4096 >= (1ll << 31) || (int64_t)256 * N * 4 >= (1ll << 31) ||
         (int64_t)M * (K / 2) >= (1ll << 31) || (int64_t)N * (K / 2) >= (1ll << 31) ||
-        (int64_t)M * N * 4 >= (1ll << 31))
+        (int64_t)std::min(M, 32) * N * 4 >= (1ll << 31))
         return fail(MBS_ERR_ARGUMENT, "problem too large for 32-bit buffer offsets");
     return MBS_OK;
 }

@@ -223,3 +223,30 @@ def test_empty_batch(dev, gold):
     torch.cuda.synchronize()
     assert_close(bf16_to_f32(m.gemm_a4w4(c.A, c.B, c.As, c.Bs)),
                  oracle.bf16_bits_to_f32(gold["c_bf16"]), "call after the empty batch")
+
+
+def test_output_past_2gib(dev):
+    """An output larger than 2^31 bytes of fp32 partials (M*N*4 > 2^31; ragged M):
+    the default plan and a forced split-K plan, whose workspace is 4.3 GB, both
+    address tiles beyond 2 GiB through 64-bit tile bases.  Rows at the 2^31-byte
+    boundaries and the last rows are checked against the oracle."""
+    import torch
+
+    import mbs_amd
+
+    M, N, K = 33000, 16384, 512
+    rng = np.random.default_rng(33)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32))
+    w = torch.from_numpy((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    c = Case.from_bf16(x.to(torch.bfloat16), w.to(torch.bfloat16))
+    rows = np.unique(np.concatenate([[0, 1, 16383, 16384, 32767, 32768, M - 2, M - 1],
+                                     rng.integers(0, M, 12)]))
+    ref = oracle.bf16_bits_to_f32(c.reference(rows))
+    names = [mbs_amd.ext().config_name(i) for i in range(mbs_amd.ext().num_configs())]
+    for cfg, splits in [(None, 0), (names.index("bdirect_256x256_w2x2"), 2)]:
+        say(f"output past 2 GiB M={M} N={N} K={K} config={cfg} splits={splits}")
+        out = c.run(config=cfg, splits=splits)
+        got = bf16_to_f32(out[torch.from_numpy(rows).to(out.device)])
+        assert_close(got, ref, f"config {cfg} splits {splits}")
+        del out
+        torch.cuda.empty_cache()
