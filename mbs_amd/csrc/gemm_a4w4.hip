@@ -263,25 +263,27 @@ double plan_cost(const Plan& pl, int M, int N, int K)
 // Measured best plans (graph-replayed timings of every configuration and
 // split count on MI355X) for the shapes of the reference's published model
 // layers, the BASELINE configurations and a few squares.  Exact matches
-// take these; every other shape goes through the cost model.
+// take these; every other shape goes through the cost model.  Three entries
+// were re-measured after the XCD tile groups became 4 rows tall (two sweeps,
+// with and without factors, same winner both times; both ranges quoted).
 struct TunedPlan {
     int M, N, K;
     const char* config;
     int splits;
 };
 const TunedPlan kTuned[] = {
-    {1024, 17408, 5120, "bdirect_192x256_w1x4", 1},  // 52.9 us
+    {1024, 17408, 5120, "bdirect_128x384_w1x4", 1},  // 54.6-55.3 us (192x256: 56.6-57.9)
     {1024, 1024, 5120, "bdirect_64x128_w1x2", 1},  // 10.7 us
     {256, 7168, 2048, "bdirect_64x128_w1x2", 1},  // 7.1 us
     {2048, 7168, 2048, "bdirect_256x256_w2x2", 1},  // 22.2 us
     {256, 4096, 7168, "bdirect_64x128_w1x2", 1},  // 13.1 us
     {2048, 4096, 7168, "bdirect_128x256_w1x4", 1},  // 30.3 us
     {256, 2112, 7168, "bdirect_64x128_w1x2", 2},  // 13.1 us
-    {2048, 2112, 7168, "bdirect_96x256_w1x4", 1},  // 24.7 us
+    {2048, 2112, 7168, "bdirect_256x128_w1x4", 1},  // 25.6-25.9 us (96x256: 27.0-27.3)
     {1000, 1280, 512, "bdirect_64x128_w1x2", 1},  // 4.9 us
     {3333, 5120, 512, "bdirect_64x128_w1x2", 1},  // 15.3 us
     {1000, 5120, 12288, "bdirect_256x128_w1x4", 1},  // 40.1 us
-    {3333, 1280, 12288, "bdirect_128x256_w1x4", 1},  // 39.4 us
+    {3333, 1280, 12288, "bdirect_256x128_w1x4", 1},  // 38.3-38.6 us (128x256: 39.2-40.0)
     {8192, 10240, 5120, "bdirect_256x256_w2x2", 1},  // 186.5 us
     {8192, 17408, 5120, "bdirect_192x256_w1x4", 1},  // 327.5 us
     {8192, 5120, 17408, "bdirect_256x256_w2x2", 1},  // 295.7 us
