@@ -113,18 +113,28 @@ quantize_bf16_kernel(const uint16_t* __restrict__ x, int rows, int K, uint8_t* _
 // infinite or NaN maximum gives 0); the row is then quantized block by block
 // after scaling by 1 + b/256, which the GEMM's factor epilogue
 // f(b) = 1/(1 + b/256) undoes.
+// Longest row the MBS kernel keeps in LDS (64 KiB of bf16).
+constexpr int kMbsStagedK = 32768;
+
+// STAGED (K * 2 bytes of dynamic LDS, K <= kMbsStagedK): the first pass
+// also keeps the row in LDS and the quantize pass reads it from there, so the
+// row is read from memory once; otherwise the quantize pass reads it again.
+template <bool STAGED>
 __global__ void __launch_bounds__(256)
 quantize_mbs_bf16_kernel(const uint16_t* __restrict__ x, int K, uint8_t* __restrict__ packed,
                          uint8_t* __restrict__ sshuf, uint8_t* __restrict__ splain,
                          uint8_t* __restrict__ factors, int snp)
 {
     __shared__ uint32_t red[4];
+    extern __shared__ __attribute__((aligned(16))) uint8_t mbs_row[];
+    i32x4* srow = reinterpret_cast<i32x4*>(mbs_row);
     const int r = blockIdx.x;
     const uint16_t* xr = x + (int64_t)r * K;
     // row maximum on the magnitude bits; a NaN maps above every number
     uint32_t amax = 0;
     for (int e = threadIdx.x * 8; e < K; e += 256 * 8) {
         const i32x4 v = *reinterpret_cast<const i32x4*>(xr + e);
+        if constexpr (STAGED) srow[e >> 3] = v;
         for (int i = 0; i < 8; ++i) {
             const uint32_t h = ((uint32_t)v[i >> 1] >> (16 * (i & 1))) & 0x7FFF;
             amax = h > amax ? h : amax;
@@ -152,7 +162,9 @@ quantize_mbs_bf16_kernel(const uint16_t* __restrict__ x, int K, uint8_t* __restr
     const int nb = K >> 5;
     const int q = threadIdx.x & 3;
     for (int b = threadIdx.x >> 2; b < nb; b += 64) {
-        const i32x4 v = *reinterpret_cast<const i32x4*>(xr + b * 32 + q * 8);
+        i32x4 v;
+        if constexpr (STAGED) v = srow[(b * 32 + q * 8) >> 3];   // written before the barrier above
+        else v = *reinterpret_cast<const i32x4*>(xr + b * 32 + q * 8);
         const uint32_t w[4] = {(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
         uint32_t mx = 0;
         for (int i = 0; i < 4; ++i) {
@@ -379,9 +391,14 @@ int mbs_quantize_mxfp4_mbs_bf16(const void* x, int rows, int K, uint8_t* packed,
             hipLaunchKernelGGL(scale_pad_kernel, dim3(blocks_for(n)), dim3(256), 0, s,
                                scale_shuffled, rows, nb, snp, (uint8_t)pad_byte);
     }
-    hipLaunchKernelGGL(quantize_mbs_bf16_kernel, dim3(rows), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(x), K, packed, scale_shuffled, scale_plain,
-                       factors, snp);
+    if (K <= kMbsStagedK)
+        hipLaunchKernelGGL(quantize_mbs_bf16_kernel<true>, dim3(rows), dim3(256), (size_t)K * 2, s,
+                           static_cast<const uint16_t*>(x), K, packed, scale_shuffled, scale_plain,
+                           factors, snp);
+    else
+        hipLaunchKernelGGL(quantize_mbs_bf16_kernel<false>, dim3(rows), dim3(256), 0, s,
+                           static_cast<const uint16_t*>(x), K, packed, scale_shuffled, scale_plain,
+                           factors, snp);
     return launched();
 }
 
