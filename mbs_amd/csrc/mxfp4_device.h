@@ -18,6 +18,7 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 #define MBS_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
@@ -328,6 +329,68 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
     typedef float f32x2 __attribute__((ext_vector_type(2)));
     const f32x2 v = {lo, hi};
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+
+// ---- MXFP4 block quantization (BASELINE configs[0] rule) ------------------
+// floor(log2(a)) of a finite a > 0 given its fp32 bits (subnormals included).
+__device__ __forceinline__ int floor_log2_bits(uint32_t u)
+{
+    const int e = (int)((u >> 23) & 0xFF);
+    if (e != 0) return e - 127;
+    return (31 - __builtin_clz(u & 0x7FFFFFu)) - 149;
+}
+
+// E8M0 scale of a block from its largest magnitude (fp32 bits, already times
+// the row multiplier m) and its NaN flag: floor(log2(amax)) - 2, biased by
+// 127 and clamped to [0, 254]; 0 for an all-zero block, 254 for an infinite
+// maximum, 255 (NaN) when the block holds a NaN.
+__device__ __forceinline__ uint32_t e8m0_of(uint32_t amax_m, bool nan)
+{
+    if (nan) return 255;
+    if (amax_m == 0) return 0;
+    if (amax_m >= 0x7F800000u) return 254;
+    const int e = floor_log2_bits(amax_m) - 2 + 127;
+    return (uint32_t)(e < 0 ? 0 : (e > 254 ? 254 : e));
+}
+
+// 2^(s - 127) for s in [0, 254] as fp32: exponent field s, or the subnormal
+// 2^-127 for s == 0.
+__device__ __forceinline__ float e8m0_value(uint32_t s)
+{
+    return s == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(s << 23);
+}
+
+// Plain MXFP4 quantization of one 32-element block held as 16 bf16 pairs
+// (w[j] = elements 2j, 2j+1): E8M0 scale -> return value, codes -> the 16
+// packed bytes in `codes` (low nibble = even element).  The codes come from
+// v_cvt_scalef32_pk_fp4_bf16: round to nearest even of x / 2^(s-127) on the
+// e2m1 grid, saturating at 6, sign kept; a block holding a NaN gets scale
+// 255 and all-zero codes (the hardware would give code 7 for the NaN).
+__device__ __forceinline__ uint32_t quantize_block32_bf16(const uint32_t w[16], i32x4* codes)
+{
+    // magnitude maximum with packed 16-bit max (v_pk_max_u16), then the halves
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 m2 = __builtin_bit_cast(u16x2, w[0] & 0x7FFF7FFFu);
+    for (int i = 1; i < 16; ++i)
+        m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, w[i] & 0x7FFF7FFFu));
+    const uint32_t mx = max((uint32_t)m2[0], (uint32_t)m2[1]);
+    const bool nan = mx > 0x7F80u;
+    const uint32_t s = e8m0_of(mx << 16, nan);
+    const float sc = e8m0_value(nan ? 127 : s);
+    i32x4 c;
+    static_for<4>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        uint32_t o = 0;
+        static_for<4>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            const uint32_t wv = w[4 * i + j];
+            o = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(o, __builtin_bit_cast(bf16x2_t, wv), sc, j);
+        });
+        c[i] = nan ? 0 : (int)o;
+    });
+    *codes = c;
+    return s;
 }
 
 }  // namespace mbs

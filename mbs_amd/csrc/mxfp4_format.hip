@@ -9,8 +9,6 @@
 
 namespace mbs {
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
 __device__ __forceinline__ int64_t flat_b(int64_t n, int64_t kp, int64_t Kp)
 {
     return (n >> 4) * (Kp * 16) + (kp >> 5) * 512 + ((kp & 31) >> 4) * 256 + (n & 15) * 16 +
@@ -21,34 +19,6 @@ __device__ __forceinline__ int64_t flat_s(int64_t r, int64_t b, int64_t snp)
 {
     return (r >> 5) * 32 * snp + (b >> 3) * 256 + (b & 3) * 64 + (r & 15) * 4 +
            ((b & 7) >> 2) * 2 + ((r & 31) >> 4);
-}
-
-// floor(log2(a)) of a finite a > 0 given its fp32 bits (subnormals included).
-__device__ __forceinline__ int floor_log2_bits(uint32_t u)
-{
-    const int e = (int)((u >> 23) & 0xFF);
-    if (e != 0) return e - 127;
-    return (31 - __builtin_clz(u & 0x7FFFFFu)) - 149;
-}
-
-// E8M0 scale of a block from its largest magnitude (fp32 bits, already times
-// the row multiplier m) and its NaN flag: floor(log2(amax)) - 2, biased by
-// 127 and clamped to [0, 254]; 0 for an all-zero block, 254 for an infinite
-// maximum, 255 (NaN) when the block holds a NaN.
-__device__ __forceinline__ uint32_t e8m0_of(uint32_t amax_m, bool nan)
-{
-    if (nan) return 255;
-    if (amax_m == 0) return 0;
-    if (amax_m >= 0x7F800000u) return 254;
-    const int e = floor_log2_bits(amax_m) - 2 + 127;
-    return (uint32_t)(e < 0 ? 0 : (e > 254 ? 254 : e));
-}
-
-// 2^(s - 127) for s in [0, 254] as fp32: exponent field s, or the subnormal
-// 2^-127 for s == 0.
-__device__ __forceinline__ float e8m0_value(uint32_t s)
-{
-    return s == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(s << 23);
 }
 
 // The e2m1 codes of the block are produced by the gfx950 scaled conversions
