@@ -74,9 +74,9 @@ def time_steps(fn, steps, warmup):
 
 def decode_bench(dev, Ms=(1, 4, 16, 32), N=8192, K=8192, copies=10, replays=20):
     """Cold (rotating copies) and warm per-launch time of the decode shapes,
-    from HIP-graph replay so host launch overhead is excluded.  Also, cold:
-    a bf16 activation through gemm_a4w4_bf16a (quantized inside the decode
-    kernel) against quantize_mxfp4 followed by gemm_a4w4 (two launches)."""
+    from HIP-graph replay so host launch overhead is excluded.  Also, cold,
+    the reference's decode flow from a bf16 activation: quantize_mxfp4, then
+    gemm_a4w4 (two launches)."""
     import torch
 
     import mbs_amd
@@ -93,11 +93,9 @@ def decode_bench(dev, Ms=(1, 4, 16, 32), N=8192, K=8192, copies=10, replays=20):
     for M in Ms:
         (A, _, As, _), (xh, _) = prepare(M, 16, K, 2, dev)
         x = xh.to(dev)
-        for mode in ("cold", "warm", "bf16a", "quantize+gemm"):
+        for mode in ("cold", "warm", "quantize+gemm"):
             idx = [0] * copies if mode == "warm" else list(range(copies))
-            if mode == "bf16a":      # bf16 activation quantized inside the decode kernel
-                run = lambda: [mbs_amd.gemm_a4w4_bf16a(x, Bc[i], Bsc[i]) for i in idx]
-            elif mode == "quantize+gemm":
+            if mode == "quantize+gemm":
                 run = lambda: [two_step(x, Bc[i], Bsc[i]) for i in idx]
             else:
                 run = lambda: [mbs_amd.gemm_a4w4(A, Bc[i], As, Bsc[i]) for i in idx]
@@ -116,11 +114,11 @@ def decode_bench(dev, Ms=(1, 4, 16, 32), N=8192, K=8192, copies=10, replays=20):
             torch.cuda.synchronize()
             us = e0.elapsed_time(e1) * 1e3 / (replays * copies)
             gbs = algo_bytes(M, N, K) / (us * 1e-6) / 1e9
-            if mode in ("cold", "warm"):
+            if mode == "quantize+gemm":
+                res.setdefault(f"M={M}", {})["cold_quantize+gemm_us"] = round(us, 3)
+            else:
                 res.setdefault(f"M={M}", {})[mode] = {
                     "us": round(us, 3), "GBps": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
-            else:
-                res.setdefault(f"M={M}", {})[f"cold_{mode}_us"] = round(us, 3)
             del g
         res[f"M={M}"]["plan"] = mbs_amd.ext().plan_name(M, N, K)
     return res

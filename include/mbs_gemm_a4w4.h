@@ -116,25 +116,6 @@ int mbs_gemm_a4w4_grouped_launch_ex(const uint8_t* A, const uint8_t* B, const ui
                                     int num_groups, void* out, int M, int N, int K, int Mpad,
                                     int scaleN_pad, float alpha, const void* bias, int config,
                                     void* stream);
-/* Decode GEMM with a bf16 activation (no counterpart in the reference, whose
- * A is always pre-quantized: test_gemm_a4w4.py:134-140 quantizes it with
- * aiter before calling the GEMM).  A: bf16 [M, K] row-major, M <= 32; B and
- * BScale as for mbs_gemm_a4w4_launch; no MBS factors (they need the row
- * maximum first).  The decode kernel quantizes each A block in registers with
- * the rule of mbs_quantize_mxfp4_bf16, so the result is bit-identical to
- * mbs_quantize_mxfp4_bf16 followed by the packed launch with the same
- * configuration and split count (mbs_gemm_a4w4_launch_ex; the plan is the
- * default one whenever that configuration has a bf16-A form, and
- * mbs_gemm_a4w4_bf16a_plan_name reports it), with one launch less.  M == 0
- * is a no-op; M > 32 is MBS_ERR_ARGUMENT.  Workspace as for the packed path:
- * mbs_gemm_a4w4_bf16a_workspace_bytes. */
-int mbs_gemm_a4w4_bf16a_launch(const void* A, const uint8_t* B, const uint8_t* BScale, void* out,
-                               int M, int N, int K, int Mpad, int scaleN_pad, float alpha,
-                               const void* bias, void* workspace, size_t workspace_bytes,
-                               void* stream);
-size_t mbs_gemm_a4w4_bf16a_workspace_bytes(int M, int N, int K);
-int mbs_gemm_a4w4_bf16a_plan_name(int M, int N, int K, char* buf, size_t buf_len);
-
 int mbs_gemm_a4w4_grouped_num_configs(void);
 const char* mbs_gemm_a4w4_grouped_config_name(int config);
 

@@ -86,18 +86,6 @@ def gemm_a4w4_grouped(A, B, A_scale, B_scale, group_offsets, A_factor=None, B_fa
                                    config, alpha, bias)
 
 
-def gemm_a4w4_bf16a(x, B, B_scale, alpha: float = 1.0, bias=None):
-    """Decode GEMM straight from a bf16 activation x [M, K].
-
-    For M <= 8 the decode kernel quantizes each block of x in registers with
-    the rule of ``quantize_mxfp4`` (one launch instead of two); larger M
-    quantizes first (measured faster there).  The result is bit-identical to
-    quantizing with ``quantize_mxfp4`` and running ``gemm_a4w4`` with the same
-    decode configuration (the default one at N = K = 8192).
-    No MBS factors (they need each row's maximum before quantization)."""
-    return ext().gemm_a4w4_bf16a(x, B, B_scale, alpha, bias)
-
-
 def quantize_mxfp4(x, shuffle: bool = True, pad_byte: int = 127):
     """bf16 [R,K] device tensor -> (packed u8 [R,K/2], E8M0 scales);
     shuffled [round_up(R,32), scaleN_pad] when ``shuffle`` else plain [R,K/32]."""

@@ -42,7 +42,6 @@ MBS_BDIRECT_SHAPES_B(MBS_BDIRECT_EXTERN)
 MBS_BDIRECT_SHAPES_C(MBS_BDIRECT_EXTERN)
 MBS_BDIRECT_SHAPES_D(MBS_BDIRECT_EXTERN)
 MBS_SKINNY_SHAPES(MBS_SKINNY_EXTERN)
-MBS_SKINNY_BF16A_SHAPES(MBS_SKINNY_BF16A_EXTERN)
 MBS_GROUPED_SHAPES(MBS_GROUPED_EXTERN)
 
 // ======================================================================
@@ -106,8 +105,6 @@ struct Config {
     // (tiled kernels) or the dead-stage/K-tail variant (persistent kernels)
     hipError_t (*launch)(const GemmArgs&, dim3, bool, bool, hipStream_t);
     bool persistent = false;  // grid capped at the resident slots; workgroups loop over units
-    // skinny only: the same kernel taking a bf16 A quantized in registers (null: none)
-    hipError_t (*launch_bf16a)(const GemmArgs&, dim3, bool, bool, hipStream_t) = nullptr;
 };
 
 const Config kConfigs[] = {
@@ -136,14 +133,13 @@ const Config kConfigs[] = {
     // eff = streaming efficiency relative to the best variant (cold N=K=8192 timings)
     {"skinny_m16_n32_w16", kSkinny, 16, 32, 1024, 1, {0.94f, 0.f, 0.f}, launch_skinny<1, 2, 16, 4>},
     {"skinny_m32_n32_w16", kSkinny, 32, 32, 1024, 1, {0.89f, 0.f, 0.f}, launch_skinny<2, 2, 16, 4>},
-    {"skinny_m16_n32_w8", kSkinny, 16, 32, 512, 2, {1.00f, 0.f, 0.f}, launch_skinny<1, 2, 8, 4>, false, launch_skinny_bf16a<1, 2, 8, 4>},
-    {"skinny_m32_n32_w8", kSkinny, 32, 32, 512, 2, {0.92f, 0.f, 0.f}, launch_skinny<2, 2, 8, 4>, false, launch_skinny_bf16a<2, 2, 8, 4>},
+    {"skinny_m16_n32_w8", kSkinny, 16, 32, 512, 2, {1.00f, 0.f, 0.f}, launch_skinny<1, 2, 8, 4>},
+    {"skinny_m32_n32_w8", kSkinny, 32, 32, 512, 2, {0.92f, 0.f, 0.f}, launch_skinny<2, 2, 8, 4>},
     {"skinny_m16_n16_w8", kSkinny, 16, 16, 512, 2, {0.91f, 0.f, 0.f}, launch_skinny<1, 1, 8, 8>},
     {"skinny_m32_n16_w8", kSkinny, 32, 16, 512, 2, {0.69f, 0.f, 0.f}, launch_skinny<2, 1, 8, 8>},
-    {"skinny_m32_n32_w4", kSkinny, 32, 32, 256, 2, {1.00f, 0.f, 0.f}, launch_skinny<2, 2, 4, 4>, false, launch_skinny_bf16a<2, 2, 4, 4>},
+    {"skinny_m32_n32_w4", kSkinny, 32, 32, 256, 2, {1.00f, 0.f, 0.f}, launch_skinny<2, 2, 4, 4>},
 };
 constexpr int kNumConfigs = (int)(sizeof(kConfigs) / sizeof(kConfigs[0]));
-constexpr int kBf16aMaxM = 32;  // the bf16-A path is the decode kernel's
 constexpr int kNumCUs = 256;
 
 struct Plan {
@@ -300,32 +296,6 @@ const TunedPlan kTuned[] = {
     {2048, 2048, 2048, "bdirect_64x256_w1x4", 1},  // 9.4 us
 };
 
-bool choose_plan(int M, int N, int K, size_t ws_avail, Plan* best);
-
-// Decode plans for a bf16 A: the default plan when its configuration has a
-// bf16-A variant (then the result is bit-identical to quantize + the default
-// launch), otherwise the cheapest configuration that has one.
-bool choose_plan_bf16a(int M, int N, int K, size_t ws_avail, Plan* best)
-{
-    if (choose_plan(M, N, K, ws_avail, best) && kConfigs[best->config].launch_bf16a) return true;
-    bool have = false;
-    double best_cost = 0;
-    for (int i = 0; i < kNumConfigs; ++i) {
-        if (!kConfigs[i].launch_bf16a) continue;
-        Plan pl;
-        if (!make_plan(i, 0, M, N, K, &pl)) continue;
-        if (pl.ws_bytes > ws_avail && !make_plan(i, 1, M, N, K, &pl)) continue;
-        if (pl.ws_bytes > ws_avail) continue;
-        const double cst = plan_cost(pl, M, N, K);
-        if (!have || cst < best_cost) {
-            *best = pl;
-            best_cost = cst;
-            have = true;
-        }
-    }
-    return have;
-}
-
 int config_index(const char* name)
 {
     for (int i = 0; i < kNumConfigs; ++i)
@@ -401,7 +371,7 @@ int validate(const uint8_t* A, const uint8_t* B, const uint8_t* As, const uint8_
 int run_plan(const Plan& pl, const uint8_t* A, const uint8_t* B, const uint8_t* As,
              const uint8_t* Bs, const uint8_t* Af, const uint8_t* Bf, void* out, int M, int N,
              int K, int snp, void* ws, size_t ws_bytes, void* stream, float alpha = 1.0f,
-             const void* bias = nullptr, bool bf16a = false)
+             const void* bias = nullptr)
 {
     const Config& c = kConfigs[pl.config];
     if (pl.ws_bytes > ws_bytes || (pl.ws_bytes && !ws))
@@ -427,7 +397,7 @@ int run_plan(const Plan& pl, const uint8_t* A, const uint8_t* B, const uint8_t* 
     const int S_total = stages_of(K);
     const bool ktail = (K % 128) != 0;
     const bool gen = c.persistent ? (ktail || pl.sps % 4 != 0 || S_total % pl.sps != 0) : ktail;
-    hipError_t e = (bf16a ? c.launch_bf16a : c.launch)(a, pl.grid, gen, pl.splits > 1, s);
+    hipError_t e = c.launch(a, pl.grid, gen, pl.splits > 1, s);
     if (e != hipSuccess) return fail(MBS_ERR_LAUNCH, std::string("launch failed: ") + hipGetErrorString(e));
     if (pl.splits > 1) {
         const int64_t quads = (int64_t)M * (N / 4);
@@ -587,47 +557,6 @@ int mbs_gemm_a4w4_grouped_launch_ex(const uint8_t* A, const uint8_t* B, const ui
     const int g = config >= 0 ? config : choose_grouped(M, N, K, num_groups);
     return run_grouped(g, A, B, AScale, BScale, AFactor, BFactor, group_offsets, num_groups, out, M,
                        N, K, scaleN_pad, stream, alpha, bias);
-}
-
-size_t mbs_gemm_a4w4_bf16a_workspace_bytes(int M, int N, int K)
-{
-    if (M < 1 || M > kBf16aMaxM || N < 16 || K < 64 || N % 16 || K % 64) return 0;
-    Plan pl;
-    if (!choose_plan_bf16a(M, N, K, (size_t)1 << 31, &pl)) return 0;
-    return pl.ws_bytes;
-}
-
-int mbs_gemm_a4w4_bf16a_plan_name(int M, int N, int K, char* buf, size_t buf_len)
-{
-    Plan pl;
-    if (M < 1 || M > kBf16aMaxM || N < 16 || K < 64 || N % 16 || K % 64 ||
-        !choose_plan_bf16a(M, N, K, (size_t)1 << 31, &pl))
-        return MBS_ERR_ARGUMENT;
-    if (buf && buf_len)
-        snprintf(buf, buf_len, "%s splits=%d grid=%ux%u ws=%zu", kConfigs[pl.config].name,
-                 pl.splits, pl.grid.x, pl.grid.y, pl.ws_bytes);
-    return MBS_OK;
-}
-
-int mbs_gemm_a4w4_bf16a_launch(const void* A, const uint8_t* B, const uint8_t* BScale, void* out,
-                               int M, int N, int K, int Mpad, int scaleN_pad, float alpha,
-                               const void* bias, void* workspace, size_t workspace_bytes,
-                               void* stream)
-{
-    set_last_error("");
-    if (M > kBf16aMaxM)
-        return fail(MBS_ERR_ARGUMENT, "bf16-A launch takes M <= " + std::to_string(kBf16aMaxM) +
-                                          " (quantize A, then mbs_gemm_a4w4_launch)");
-    // the same checks as the packed path (A's K/2 bytes stand in for its 2K)
-    int st = validate(static_cast<const uint8_t*>(A), B, B, BScale, nullptr, nullptr, out, M, N,
-                      K, Mpad, scaleN_pad);
-    if (st != MBS_OK || M == 0) return st;
-    if (!(alpha == alpha)) return fail(MBS_ERR_ARGUMENT, "alpha is NaN");
-    Plan pl;
-    if (!choose_plan_bf16a(M, N, K, workspace ? workspace_bytes : 0, &pl))
-        return fail(MBS_ERR_CONFIG, "no bf16-A configuration fits this problem");
-    return run_plan(pl, static_cast<const uint8_t*>(A), B, nullptr, BScale, nullptr, nullptr, out,
-                    M, N, K, scaleN_pad, workspace, workspace_bytes, stream, alpha, bias, true);
 }
 
 int mbs_gemm_a4w4_grouped_num_configs(void) { return kNumGrouped; }

@@ -185,60 +185,6 @@ std::tuple<at::Tensor, at::Tensor> quantize_mxfp4(at::Tensor x, bool shuffle, in
     return {packed, scales};
 }
 
-// Decode GEMM with a bf16 activation x [M, K] (no reference counterpart: its
-// A is quantized by aiter before the call).  M <= kFusedMaxM: the decode
-// kernel quantizes x in registers, one launch.  Larger M: quantize_mxfp4,
-// then gemm_a4w4 (measured faster there: the in-kernel quantization reads A
-// at 4x the packed size from L2 and adds its VALU work to every wave).
-// Either way the result is bit-identical to quantize-then-GEMM with the same
-// decode configuration (the default one for N = K = 8192).
-constexpr int64_t kFusedMaxM = 8;
-at::Tensor gemm_a4w4_bf16a(at::Tensor x, at::Tensor B, at::Tensor B_scale, double alpha,
-                           c10::optional<at::Tensor> bias)
-{
-    TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.scalar_type() == at::kBFloat16,
-                "gemm_a4w4_bf16a: x must be a 2D bf16 device tensor");
-    if (x.size(0) > kFusedMaxM) {
-        auto q = quantize_mxfp4(x, true, 127);
-        return gemm_a4w4(std::get<0>(q), B, std::get<1>(q), B_scale, c10::nullopt, c10::nullopt,
-                         alpha, bias);
-    }
-    TORCH_CHECK(B.is_cuda() && B.dim() == 2 && B.element_size() == 1 && B_scale.is_cuda() &&
-                    B_scale.element_size() == 1,
-                "gemm_a4w4_bf16a: B and B_scale must be 1-byte device tensors, B 2D");
-    TORCH_CHECK(B.device() == x.device() && B_scale.device() == x.device(),
-                "gemm_a4w4_bf16a: all operands must be on the same device");
-    auto xc = x.contiguous();
-    auto Bb = as_bytes(B), Bs = as_bytes(B_scale);
-    const int64_t M = xc.size(0), K = xc.size(1), N = Bb.size(0);
-    TORCH_CHECK(Bb.size(1) * 2 == K, "gemm_a4w4_bf16a: B must be [N, K/2], got K/2 = ", Bb.size(1),
-                " for K = ", K);
-    TORCH_CHECK(K % 64 == 0, "gemm_a4w4_bf16a: K must be a multiple of 64, got ", K);
-    TORCH_CHECK(N % 16 == 0, "gemm_a4w4_bf16a: N must be a multiple of 16, got ", N);
-    const int64_t Mpad = round_up(M, 32), snp = scale_pad(K);
-    TORCH_CHECK(Bs.numel() >= round_up(N, 32) * snp, "gemm_a4w4_bf16a: B_scale must hold at least ",
-                round_up(N, 32) * snp, " bytes (round_up(N,32) * scaleN_pad), got ", Bs.numel());
-    c10::DeviceGuard guard(x.device());
-    auto out = torch::empty({Mpad, N}, torch::TensorOptions().dtype(torch::kBFloat16).device(x.device()));
-    const size_t ws = mbs_gemm_a4w4_bf16a_workspace_bytes((int)M, (int)N, (int)K);
-    at::Tensor wst;
-    if (ws) wst = torch::empty({(int64_t)ws}, torch::TensorOptions().dtype(torch::kByte).device(x.device()));
-    at::Tensor bu;
-    if (bias.has_value()) {
-        TORCH_CHECK(bias->is_cuda() && bias->device() == x.device() &&
-                        bias->scalar_type() == at::kBFloat16 && bias->numel() == N,
-                    "gemm_a4w4_bf16a: bias must be a bf16 device tensor of N entries");
-        bu = bias->contiguous();
-    }
-    check_status(mbs_gemm_a4w4_bf16a_launch(xc.data_ptr(), Bb.data_ptr<uint8_t>(),
-                                            Bs.data_ptr<uint8_t>(), out.data_ptr(), (int)M, (int)N,
-                                            (int)K, (int)Mpad, (int)snp, (float)alpha,
-                                            bu.defined() ? bu.data_ptr() : nullptr,
-                                            ws ? wst.data_ptr() : nullptr, ws, current_stream(x)),
-                 "gemm_a4w4_bf16a");
-    return out.narrow(0, 0, M);
-}
-
 // MBS quantization: (packed, scales, factor bytes [R]) -- rows scaled by
 // their MBS multipliers before quantization; pass the factors to gemm_a4w4.
 std::tuple<at::Tensor, at::Tensor, at::Tensor> quantize_mxfp4_mbs(at::Tensor x, bool shuffle,
@@ -453,11 +399,6 @@ PYBIND11_MODULE(mbs_gemm_a4w4, m)
           pybind11::arg("A_scale"), pybind11::arg("B_scale"),
           pybind11::arg("A_factor") = pybind11::none(), pybind11::arg("B_factor") = pybind11::none(),
           pybind11::arg("alpha") = 1.0, pybind11::arg("bias") = pybind11::none());
-    m.def("gemm_a4w4_bf16a", &gemm_a4w4_bf16a,
-          "decode GEMM with a bf16 activation quantized in the kernel (M <= 32; larger M "
-          "quantizes first): bit-identical to gemm_a4w4(*quantize_mxfp4(x), B, B_scale)",
-          pybind11::arg("x"), pybind11::arg("B"), pybind11::arg("B_scale"),
-          pybind11::arg("alpha") = 1.0, pybind11::arg("bias") = pybind11::none());
     m.def("quantize_mxfp4", &quantize_mxfp4, "bf16 -> (packed e2m1, E8M0 scales)",
           pybind11::arg("x"), pybind11::arg("shuffle") = true, pybind11::arg("pad_byte") = 127);
     m.def("quantize_mxfp4_mbs", &quantize_mxfp4_mbs,
@@ -487,12 +428,6 @@ PYBIND11_MODULE(mbs_gemm_a4w4, m)
     m.def("grouped_config_name",
           [](int64_t c) { return std::string(mbs_gemm_a4w4_grouped_config_name((int)c)); });
     m.def("plan_name", &plan_name, "kernel plan the heuristic picks for (M, N, K)");
-    m.def("bf16a_plan_name", [](int64_t M, int64_t N, int64_t K) {
-        char buf[160];
-        check_status(mbs_gemm_a4w4_bf16a_plan_name((int)M, (int)N, (int)K, buf, sizeof(buf)),
-                     "bf16a_plan_name");
-        return std::string(buf);
-    }, "decode plan of gemm_a4w4_bf16a for (M <= 32, N, K)");
     m.def("num_configs", []() { return mbs_gemm_a4w4_num_configs(); });
     m.def("config_name", [](int64_t c) { return std::string(mbs_gemm_a4w4_config_name((int)c)); });
     m.def("workspace_bytes", [](int64_t M, int64_t N, int64_t K) {

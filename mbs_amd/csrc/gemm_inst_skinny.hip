@@ -4,5 +4,4 @@
 
 namespace mbs {
 MBS_SKINNY_SHAPES(MBS_SKINNY_INST)
-MBS_SKINNY_BF16A_SHAPES(MBS_SKINNY_BF16A_INST)
 }  // namespace mbs

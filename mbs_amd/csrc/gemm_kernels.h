@@ -1178,18 +1178,10 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
 // once, with the non-temporal policy; up to U stages of B, A and scales
 // are in flight per wave.  Waves reduce their partial tiles through LDS
 // in a fixed order (deterministic), then NF*MT waves run the epilogue.
-//
-// BF16A: A is bf16 [M, K] (no A scales) and each lane quantizes, in
-// registers, exactly the block its MFMA fragment holds (row 16m + lane%16,
-// K-block lane/16 of the stage) with the plain quantizer's rule.  Codes and
-// scale bytes equal the quantizer's, so the products and their order are
-// those of the pre-quantized path and the output is bit-identical to
-// quantize-then-GEMM, without the quantizer's launch.
-template <int MT, int NF, int NWK, int U, bool SPLIT, bool BF16A = false>
+template <int MT, int NF, int NWK, int U, bool SPLIT>
 __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
 {
     static_assert(U % 2 == 0, "batch must cover whole 256-K scale groups");
-    static_assert(!BF16A || (NWK <= 8 && U <= 4), "raw bf16 fragments must fit the registers");
     static_assert(NF == 1 || NF == 2, "one 32-row scale group per workgroup");
     static_assert(NF * MT <= NWK, "one epilogue wave per output fragment");
     __shared__ f32x4 red[NWK][NF * MT][64];
@@ -1212,8 +1204,8 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
     const int nfrag = min(NF, (p.N - n0) >> 4);
     const uint32_t fstride = (uint32_t)K * 8;  // bytes of one 16-row fragment column
     const rsrc_t rB = make_rsrc(p.B + (size_t)(n0 >> 4) * fstride, (uint32_t)nfrag * fstride);
-    const rsrc_t rA = make_rsrc(p.A, (uint32_t)(p.M * (BF16A ? 2 * K : Kp)));
-    const rsrc_t rAs = make_rsrc(p.As, BF16A ? 0u : (uint32_t)(32 * p.snp));
+    const rsrc_t rA = make_rsrc(p.A, (uint32_t)(p.M * Kp));
+    const rsrc_t rAs = make_rsrc(p.As, (uint32_t)(32 * p.snp));
     const rsrc_t rBs = make_rsrc(p.Bs + (size_t)(n0 >> 5) * 32 * p.snp, (uint32_t)(32 * p.snp));
     const bool hi_lane = lane >= 32;
     const bool ktail = (K & 127) != 0;
@@ -1228,7 +1220,6 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
 
     for (int st = my_begin; st < my_end; st += U) {
         i32x4 b[U][NF], a[U][MT];
-        i32x4 ar[BF16A ? U : 1][BF16A ? MT : 1][4];  // BF16A: the raw 64 bytes of each fragment
         int sb[U / 2], sa[U / 2];
         // Scales first: loads return in issue order, so stage u's MFMAs then
         // wait only for stage u's B and A, and the MFMAs trail the stream
@@ -1237,7 +1228,7 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
             const int g = (st >> 1) + v;
             const bool ok = st + 2 * v < my_end;
             sb[v] = load4(rBs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
-            if constexpr (!BF16A) sa[v] = load4(rAs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
+            sa[v] = load4(rAs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
         });
         static_for<U>([&](auto u) {
             const int s = st + u;
@@ -1247,43 +1238,15 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
                 b[u][f] = load16nt(rB, zap ? kOOB : (uint32_t)(f * fstride + s * 1024 + lane * 16));
             });
             static_for<MT>([&](auto m) {
-                if constexpr (BF16A) {
-                    const uint32_t o = (uint32_t)(((16 * m + (lane & 15)) * K + s * 128 +
-                                                   (lane >> 4) * 32) * 2);
-                    static_for<4>([&](auto i) {
-                        ar[u][m][i] = load16(rA, zap ? kOOB : o + 16 * (uint32_t)decltype(i)::value);
-                    });
-                } else {
-                    a[u][m] = load16(rA, zap ? kOOB
-                                             : (uint32_t)((16 * m + (lane & 15)) * Kp + s * 64 +
-                                                          (lane >> 4) * 16));
-                }
+                a[u][m] = load16(rA, zap ? kOOB
+                                         : (uint32_t)((16 * m + (lane & 15)) * Kp + s * 64 +
+                                                      (lane >> 4) * 16));
             });
         });
         // Every load of the batch is issued before the first MFMA; left to
         // itself the scheduler interleaves them with the MFMAs and the wave
         // keeps only a fraction of its batch in flight.
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (BF16A) {
-            // codes and scale bytes of every fragment; the scale of fragment
-            // m at stage parity h is byte m + 2h of the lane's group dword,
-            // where the shuffled A scales would have put it
-            static_for<U / 2>([&](auto v) { sa[v] = 0; });
-            static_for<U>([&](auto u) {
-                constexpr int h = u & 1;
-                static_for<MT>([&](auto m) {
-                    uint32_t w[16];
-                    static_for<4>([&](auto i) {
-                        static_for<4>([&](auto j) {
-                            w[4 * decltype(i)::value + decltype(j)::value] =
-                                (uint32_t)ar[u][m][decltype(i)::value][decltype(j)::value];
-                        });
-                    });
-                    const uint32_t sc = quantize_block32_bf16(w, &a[u][m]);
-                    sa[u / 2] |= (int)(sc << (8 * (m + 2 * h)));
-                });
-            });
-        }
         static_for<U>([&](auto u) {
             constexpr int h = u & 1;
             const int s = st + u;
@@ -1393,15 +1356,6 @@ hipError_t launch_skinny(const GemmArgs& a, dim3 grid, bool, bool split, hipStre
     return hipGetLastError();
 }
 
-// The same kernels with a bf16 A quantized in registers (a.A: bf16 [M, K]).
-template <int MT, int NF, int NWK, int U>
-hipError_t launch_skinny_bf16a(const GemmArgs& a, dim3 grid, bool, bool split, hipStream_t s)
-{
-    if (split) hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, true, true>), grid, dim3(64 * NWK), 0, s, a);
-    else hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, false, true>), grid, dim3(64 * NWK), 0, s, a);
-    return hipGetLastError();
-}
-
 using T256x256 = TileShape<256, 256, 2, 2>;
 using T256x128 = TileShape<256, 128, 2, 2>;
 using T128x256 = TileShape<128, 256, 2, 2>;
@@ -1439,10 +1393,6 @@ using B128x256w14 = BdShape<128, 256, 1, 4>;
 #define MBS_TILED_INST(T) template hipError_t launch_tiled<T>(MBS_LAUNCH_SIG);
 #define MBS_BDIRECT_INST(T) template hipError_t launch_bdirect<T>(MBS_LAUNCH_SIG);
 #define MBS_SKINNY_INST(a, b, c, d) template hipError_t launch_skinny<a, b, c, d>(MBS_LAUNCH_SIG);
-// bf16-A decode variants: the shapes with at most 8 waves and 4-stage batches
-#define MBS_SKINNY_BF16A_SHAPES(X) X(1, 2, 8, 4) X(2, 2, 8, 4) X(2, 2, 4, 4)
-#define MBS_SKINNY_BF16A_INST(a, b, c, d) template hipError_t launch_skinny_bf16a<a, b, c, d>(MBS_LAUNCH_SIG);
-#define MBS_SKINNY_BF16A_EXTERN(a, b, c, d) extern template hipError_t launch_skinny_bf16a<a, b, c, d>(MBS_LAUNCH_SIG);
 #define MBS_GROUPED_INST(T) template hipError_t launch_bdirect_grouped<T>(MBS_LAUNCH_SIG);
 #define MBS_GROUPED_EXTERN(T) extern template hipError_t launch_bdirect_grouped<T>(MBS_LAUNCH_SIG);
 #define MBS_TILED_EXTERN(T) extern template hipError_t launch_tiled<T>(MBS_LAUNCH_SIG);

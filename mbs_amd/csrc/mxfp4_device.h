@@ -361,36 +361,4 @@ __device__ __forceinline__ float e8m0_value(uint32_t s)
     return s == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(s << 23);
 }
 
-// Plain MXFP4 quantization of one 32-element block held as 16 bf16 pairs
-// (w[j] = elements 2j, 2j+1): E8M0 scale -> return value, codes -> the 16
-// packed bytes in `codes` (low nibble = even element).  The codes come from
-// v_cvt_scalef32_pk_fp4_bf16: round to nearest even of x / 2^(s-127) on the
-// e2m1 grid, saturating at 6, sign kept; a block holding a NaN gets scale
-// 255 and all-zero codes (the hardware would give code 7 for the NaN).
-__device__ __forceinline__ uint32_t quantize_block32_bf16(const uint32_t w[16], i32x4* codes)
-{
-    // magnitude maximum with packed 16-bit max (v_pk_max_u16), then the halves
-    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-    u16x2 m2 = __builtin_bit_cast(u16x2, w[0] & 0x7FFF7FFFu);
-    for (int i = 1; i < 16; ++i)
-        m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, w[i] & 0x7FFF7FFFu));
-    const uint32_t mx = max((uint32_t)m2[0], (uint32_t)m2[1]);
-    const bool nan = mx > 0x7F80u;
-    const uint32_t s = e8m0_of(mx << 16, nan);
-    const float sc = e8m0_value(nan ? 127 : s);
-    i32x4 c;
-    static_for<4>([&](auto I) {
-        constexpr int i = decltype(I)::value;
-        uint32_t o = 0;
-        static_for<4>([&](auto J) {
-            constexpr int j = decltype(J)::value;
-            const uint32_t wv = w[4 * i + j];
-            o = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(o, __builtin_bit_cast(bf16x2_t, wv), sc, j);
-        });
-        c[i] = nan ? 0 : (int)o;
-    });
-    *codes = c;
-    return s;
-}
-
 }  // namespace mbs

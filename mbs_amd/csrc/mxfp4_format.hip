@@ -38,17 +38,25 @@ __device__ __forceinline__ int64_t flat_s(int64_t r, int64_t b, int64_t snp)
 // contiguously), the quad combines its magnitudes into the block maximum, and
 // each lane converts its 8 elements into one dword of packed output
 // (v_cvt_scalef32_pk_fp4_bf16 straight from the bf16 pairs).  blockIdx.x:
-// group of 4 rows (threadIdx.y), blockIdx.y: group of 64 chunks.
+// group of 4 rows (threadIdx.y), blockIdx.y: group of 64 chunks.  With a
+// shuffled scale buffer the grid also covers its padding (rows up to
+// round_up(rows, 32), blocks up to scaleN_pad), whose entries get `pad`, so
+// one launch fills the whole buffer.
 __global__ void __launch_bounds__(256)
 quantize_bf16_kernel(const uint16_t* __restrict__ x, int rows, int K, uint8_t* __restrict__ packed,
-                     uint8_t* __restrict__ sshuf, uint8_t* __restrict__ splain, int snp)
+                     uint8_t* __restrict__ sshuf, uint8_t* __restrict__ splain, int snp, uint8_t pad)
 {
     const int nc = K >> 3;                               // 16-byte chunks per row
     const int j = blockIdx.y * 64 + threadIdx.x;          // chunk in the row
     const int r = blockIdx.x * 4 + threadIdx.y;           // row (uniform per wave)
-    // nc % 4 == 0 and quads are 4-aligned: whole quads leave together, so
-    // the quad exchanges below only read active lanes.
-    if (r >= rows || j >= nc) return;
+    // nc % 4 == 0 and quads are 4-aligned: whole quads take the same branch,
+    // so the quad exchanges below only read active lanes.
+    if (r >= rows || j >= nc) {
+        const int rows_pad = (rows + 31) & ~31;
+        if (sshuf && r < rows_pad && j < 4 * snp && (threadIdx.x & 3) == 0)
+            sshuf[flat_s(r, j >> 2, snp)] = pad;
+        return;
+    }
     const i32x4 v = *reinterpret_cast<const i32x4*>(x + (int64_t)r * K + (int64_t)j * 8);
     // magnitude maximum on the 15 magnitude bits: a NaN orders above inf
     uint32_t mx = 0;
@@ -331,16 +339,12 @@ int mbs_quantize_mxfp4_bf16(const void* x, int rows, int K, uint8_t* packed,
     (void)hipGetLastError();
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int snp = scale_pad_of(K);
-    const int nb = K / 32;
-    if (scale_shuffled) {
-        const int64_t n = (int64_t)((rows + 31) & ~31) * snp;
-        if ((rows % 32) || nb != snp)
-            hipLaunchKernelGGL(scale_pad_kernel, dim3(blocks_for(n)), dim3(256), 0, s,
-                               scale_shuffled, rows, nb, snp, (uint8_t)pad_byte);
-    }
-    hipLaunchKernelGGL(quantize_bf16_kernel, dim3((rows + 3) / 4, (K / 8 + 63) / 64), dim3(64, 4),
-                       0, s, static_cast<const uint16_t*>(x), rows, K, packed, scale_shuffled,
-                       scale_plain, snp);
+    // with a shuffled buffer the grid also spans its padding rows and blocks
+    const int grid_rows = scale_shuffled ? ((rows + 31) & ~31) : rows;
+    const int grid_chunks = scale_shuffled ? 4 * snp : K / 8;
+    hipLaunchKernelGGL(quantize_bf16_kernel, dim3((grid_rows + 3) / 4, (grid_chunks + 63) / 64),
+                       dim3(64, 4), 0, s, static_cast<const uint16_t*>(x), rows, K, packed,
+                       scale_shuffled, scale_plain, snp, (uint8_t)pad_byte);
     return launched();
 }
 
