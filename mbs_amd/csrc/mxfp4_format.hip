@@ -99,14 +99,23 @@ constexpr int kMbsStagedK = 32768;
 // row is read from memory once; otherwise the quantize pass reads it again.
 template <bool STAGED>
 __global__ void __launch_bounds__(256)
-quantize_mbs_bf16_kernel(const uint16_t* __restrict__ x, int K, uint8_t* __restrict__ packed,
+quantize_mbs_bf16_kernel(const uint16_t* __restrict__ x, int rows, int K, uint8_t* __restrict__ packed,
                          uint8_t* __restrict__ sshuf, uint8_t* __restrict__ splain,
-                         uint8_t* __restrict__ factors, int snp)
+                         uint8_t* __restrict__ factors, int snp, uint8_t pad)
 {
     __shared__ uint32_t red[4];
     extern __shared__ __attribute__((aligned(16))) uint8_t mbs_row[];
     i32x4* srow = reinterpret_cast<i32x4*>(mbs_row);
     const int r = blockIdx.x;
+    // With a shuffled scale buffer the grid spans round_up(rows, 32) rows:
+    // a padding row's workgroup only writes its pad bytes; every row writes
+    // its padding blocks [K/32, scaleN_pad).
+    if (r >= rows) {
+        for (int b = threadIdx.x; b < snp; b += 256) sshuf[flat_s(r, b, snp)] = pad;
+        return;
+    }
+    if (sshuf)
+        for (int b = (K >> 5) + threadIdx.x; b < snp; b += 256) sshuf[flat_s(r, b, snp)] = pad;
     const uint16_t* xr = x + (int64_t)r * K;
     // row maximum on the magnitude bits; a NaN maps above every number
     uint32_t amax = 0;
@@ -169,16 +178,6 @@ quantize_mbs_bf16_kernel(const uint16_t* __restrict__ x, int K, uint8_t* __restr
     }
 }
 
-// Padding entries of a shuffled scale buffer (rows >= R or blocks >= nb).
-__global__ void __launch_bounds__(256)
-scale_pad_kernel(uint8_t* __restrict__ sshuf, int rows, int nb, int snp, uint8_t pad)
-{
-    const int rows_pad = (rows + 31) & ~31;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (int64_t)rows_pad * snp) return;
-    const int r = (int)(i / snp), b = (int)(i - (int64_t)r * snp);
-    if (r >= rows || b >= nb) sshuf[flat_s(r, b, snp)] = pad;
-}
 
 __global__ void __launch_bounds__(256)
 shuffle_scales_kernel(const uint8_t* __restrict__ plain, uint8_t* __restrict__ out, int rows,
@@ -358,21 +357,15 @@ int mbs_quantize_mxfp4_mbs_bf16(const void* x, int rows, int K, uint8_t* packed,
     (void)hipGetLastError();
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int snp = scale_pad_of(K);
-    const int nb = K / 32;
-    if (scale_shuffled) {
-        const int64_t n = (int64_t)((rows + 31) & ~31) * snp;
-        if ((rows % 32) || nb != snp)
-            hipLaunchKernelGGL(scale_pad_kernel, dim3(blocks_for(n)), dim3(256), 0, s,
-                               scale_shuffled, rows, nb, snp, (uint8_t)pad_byte);
-    }
+    const int grid = scale_shuffled ? ((rows + 31) & ~31) : rows;  // padding rows included
     if (K <= kMbsStagedK)
-        hipLaunchKernelGGL(quantize_mbs_bf16_kernel<true>, dim3(rows), dim3(256), (size_t)K * 2, s,
-                           static_cast<const uint16_t*>(x), K, packed, scale_shuffled, scale_plain,
-                           factors, snp);
+        hipLaunchKernelGGL(quantize_mbs_bf16_kernel<true>, dim3(grid), dim3(256), (size_t)K * 2, s,
+                           static_cast<const uint16_t*>(x), rows, K, packed, scale_shuffled,
+                           scale_plain, factors, snp, (uint8_t)pad_byte);
     else
-        hipLaunchKernelGGL(quantize_mbs_bf16_kernel<false>, dim3(rows), dim3(256), 0, s,
-                           static_cast<const uint16_t*>(x), K, packed, scale_shuffled, scale_plain,
-                           factors, snp);
+        hipLaunchKernelGGL(quantize_mbs_bf16_kernel<false>, dim3(grid), dim3(256), 0, s,
+                           static_cast<const uint16_t*>(x), rows, K, packed, scale_shuffled,
+                           scale_plain, factors, snp, (uint8_t)pad_byte);
     return launched();
 }
 
