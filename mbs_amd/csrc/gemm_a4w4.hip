@@ -434,8 +434,27 @@ int grouped_units_bound(const Config& c, int M, int N, int E)
 
 // Config choice: the dense cost model at the tile count the experts' padded
 // row blocks give on average (half a tile of padding per expert).
+// Measured best grouped configurations (graph-replayed, every configuration)
+// for configs[3]'s expert shapes at 8 experts x 256 tokens; exact matches on
+// (M, N, K, E) take these, everything else goes through the cost model.
+struct TunedGrouped {
+    int M, N, K, E;
+    const char* dense;
+};
+const TunedGrouped kTunedGrouped[] = {
+    // two sweeps each: us of the chosen / the cost model's pick (64x256 or 64x128)
+    {2048, 7168, 2048, 8, "bdirect_256x256_w2x2"},  // 25.7, 25.1 / 27.8
+    {2048, 4096, 7168, 8, "bdirect_128x256_w1x4"},  // 39.3, 34.5 / 44.3 (64x256: 39.0, 37.3)
+    {2048, 2112, 7168, 8, "bdirect_128x256_w1x4"},  // 27.1, 27.0 / 29.7
+};
+
 int choose_grouped(int M, int N, int K, int E)
 {
+    for (const TunedGrouped& t : kTunedGrouped) {
+        if (t.M != M || t.N != N || t.K != K || t.E != E) continue;
+        for (int g = 0; g < kNumGrouped; ++g)
+            if (std::strcmp(kGrouped[g].dense, t.dense) == 0) return g;
+    }
     int best = 0;
     double best_cost = 0;
     for (int g = 0; g < kNumGrouped; ++g) {
