@@ -86,6 +86,8 @@ def test_grouped_matches_dense_per_expert(dev, config, rows, N, K):
     ([32] * 24, 256, 512, False),              # many small experts (one partial tile each)
     ([96, 160, 0, 32, 224], 768, 1088, True),  # factors, K % 128 == 64 (K tail)
     ([0, 0, 288], 1024, 4096, True),           # leading empty experts
+    ([256] * 8, 7168, 2048, False),            # configs[3] expert shapes: the tuned-table
+    ([256] * 8, 2112, 7168, False),            # plans (256x256 and 128x256)
 ])
 def test_grouped_default_plan(dev, rows, N, K, factors):
     import torch
