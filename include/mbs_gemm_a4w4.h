@@ -22,7 +22,9 @@
  *   out      [Mpad, N]  bf16, Mpad = round_up(M,32); rows >= M untouched.
  *   scaleN_pad = round_up(ceil(K/32), 8).
  * Requirements: M >= 0, N % 16 == 0, K % 64 == 0 (the (16,16) preshuffle
- * needs K/2 % 32 == 0), all pointers device-accessible.  Size limits (32-bit
+ * needs K/2 % 32 == 0), all pointers device-accessible; A, B, the scales,
+ * out, the workspace and a bias 16-byte aligned, the factors 4-byte aligned
+ * (MBS_ERR_ARGUMENT otherwise).  Size limits (32-bit
  * buffer offsets): M*K/2 and N*K/2 below 2^31 bytes, 256*N*4 below 2^31; the
  * output itself may exceed 2^31 bytes (it is addressed per tile).  M == 0 (an empty
  * batch, e.g. an expert without tokens) validates the other arguments and
@@ -75,9 +77,10 @@ int mbs_gemm_a4w4_launch(const uint8_t* A, const uint8_t* B, const uint8_t* ASca
 /* mbs_gemm_a4w4_launch (config < 0) or mbs_gemm_a4w4_launch_config with an
  * affine epilogue:  out[m][n] = bf16( C[m][n] * (alpha * f(AFactor[m]) *
  * f(BFactor[n])) + bias[n] )  in fp32, bias bf16 [N] or NULL.  alpha = 1 with
- * no bias gives exactly mbs_gemm_a4w4_launch's bytes.  The alpha/bias
- * epilogue of the aiter assembly kernel the reference compares against
- * (asm_vs_wg_kernel.md:85-87); the reference's own launcher has none. */
+ * no bias gives exactly mbs_gemm_a4w4_launch's bytes.  The bias follows
+ * the aiter GEMM the reference's harness calls next to its own kernel
+ * (test_gemm_a4w4.py:95-123, which passes a bias argument); the reference's
+ * own launcher has neither alpha nor bias. */
 int mbs_gemm_a4w4_launch_ex(int config, int splits, const uint8_t* A, const uint8_t* B,
                             const uint8_t* AScale, const uint8_t* BScale, const uint8_t* AFactor,
                             const uint8_t* BFactor, void* out, int M, int N, int K, int Mpad,
@@ -94,9 +97,11 @@ int mbs_gemm_a4w4_launch_ex(int config, int splits, const uint8_t* A, const uint
  * group_offsets: device int32 [E+1], group_offsets[0] = 0, non-decreasing,
  * every entry a multiple of 32 (pad each expert's token block, as MoE
  * routing usually does), group_offsets[E] <= M; it is read by the kernel,
- * not checked on the host (offsets outside [0, M] are clamped into it on the
- * device, so no store leaves the output).  Rows past group_offsets[E] are
- * not written.
+ * not checked on the host.  Offsets outside [0, M] are clamped into it on
+ * the device, so no store leaves the output; an expert whose first row is
+ * not a multiple of 32 is skipped (its rows are not written: the shuffled A
+ * scales come in 32-row groups).  mbs_gemm_a4w4_check_groups reports both
+ * cases.  Rows past group_offsets[E] are not written.
  * config: -1 for the heuristic, else 0 <= config <
  * mbs_gemm_a4w4_grouped_num_configs().  Each expert's rows give the same
  * bytes as mbs_gemm_a4w4_launch on that expert alone.  No counterpart in the
@@ -116,6 +121,16 @@ int mbs_gemm_a4w4_grouped_launch_ex(const uint8_t* A, const uint8_t* B, const ui
                                     int num_groups, void* out, int M, int N, int K, int Mpad,
                                     int scaleN_pad, float alpha, const void* bias, int config,
                                     void* stream);
+/* Report on a grouped launch's device offsets (one small kernel; the
+ * caller reads `status` after the stream reaches it):
+ *   status[0] = non-empty experts whose first row is not a multiple of 32
+ *               (the grouped kernels skip them),
+ *   status[1] = entries the kernels clamp: group_offsets[0] != 0, an entry
+ *               outside [0, M], or a decrease.
+ * `status` is 2 device uint32 words, written (not accumulated).  No
+ * counterpart in the reference. */
+int mbs_gemm_a4w4_check_groups(const int* group_offsets, int num_groups, int M, uint32_t* status,
+                               void* stream);
 int mbs_gemm_a4w4_grouped_num_configs(void);
 const char* mbs_gemm_a4w4_grouped_config_name(int config);
 

@@ -48,11 +48,18 @@ def ext():
 
 
 def clib() -> ctypes.CDLL:
-    """ctypes handle on ``libmbs_gemm_kernel.so`` (the C ABI)."""
+    """ctypes handle on ``libmbs_gemm_kernel.so`` (the C ABI).
+
+    torch is imported first: torch ships its own HIP runtime under the same
+    soname (libamdhip64.so.7) as the ROCm one this library links against, and
+    whichever is loaded first serves the whole process.  Loading torch first
+    keeps this library on the runtime that owns torch's memory and streams."""
     global _clib
     if _clib is None:
         if not os.path.exists(KERNEL_LIB_PATH):
             raise ImportError(f"{KERNEL_LIB_PATH} not built; run `python -m mbs_amd._build`")
+        import torch  # noqa: F401  (see above)
+
         _clib = ctypes.CDLL(KERNEL_LIB_PATH)
     return _clib
 
@@ -71,7 +78,7 @@ def gemm_a4w4(A, B, A_scale, B_scale, A_factor=None, B_factor=None, alpha: float
 
 
 def gemm_a4w4_grouped(A, B, A_scale, B_scale, group_offsets, A_factor=None, B_factor=None,
-                      config: int = -1, alpha: float = 1.0, bias=None):
+                      config: int = -1, alpha: float = 1.0, bias=None, validate: bool = False):
     """Grouped (mixture-of-experts) GEMM in one launch.
 
     Expert e owns rows [group_offsets[e], group_offsets[e+1]) of A and of the
@@ -81,9 +88,19 @@ def gemm_a4w4_grouped(A, B, A_scale, B_scale, group_offsets, A_factor=None, B_fa
     token block), last <= M.  Each expert's rows equal ``gemm_a4w4`` of that
     expert alone.  Rows past the last offset are not written.  ``alpha`` and
     ``bias`` (bf16 [E, N] or [E*N], expert e's row added to its rows) give the
-    affine epilogue of ``gemm_a4w4``."""
+    affine epilogue of ``gemm_a4w4``.  Host offsets are checked on the host;
+    device offsets are read by the kernel unchecked (an expert starting off a
+    32-row boundary is skipped, out-of-range offsets are clamped) unless
+    ``validate`` asks for a device-side check first (it synchronises)."""
     return ext().gemm_a4w4_grouped(A, B, A_scale, B_scale, group_offsets, A_factor, B_factor,
-                                   config, alpha, bias)
+                                   config, alpha, bias, validate)
+
+
+def check_groups(group_offsets, M: int):
+    """(non-empty experts whose first row is not a multiple of 32, offsets
+    outside [0, M] or decreasing) of an int32 device offset vector;
+    synchronises the stream."""
+    return ext().check_groups(group_offsets, M)
 
 
 def quantize_mxfp4(x, shuffle: bool = True, pad_byte: int = 127):

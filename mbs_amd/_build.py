@@ -11,7 +11,10 @@ Products (under ``mbs_amd/lib/``):
   rpath so the pair travels together.
 
 Run ``python -m mbs_amd._build`` (or ``__graft_entry__.build()``).  Every call
-rebuilds.
+rebuilds.  ``python -m mbs_amd._build --phase-timer`` builds
+``libmbs_gemm_phase.so`` instead: the same kernels with the in-kernel phase
+timer (``MBS_PHASE_TIMER=1``, ``include/mbs_phase_timer.h``), a measurement
+tool.
 """
 from __future__ import annotations
 
@@ -34,7 +37,7 @@ ARCH = "gfx950"
 # (gemm_inst_*.hip) so that they compile in parallel.
 HIP_SOURCES = [
     "gemm_inst_bdirect_c.hip", "gemm_inst_bdirect_d.hip", "gemm_inst_bdirect_a.hip",
-    "gemm_inst_bdirect_b.hip", "gemm_inst_grouped.hip", "gemm_inst_tiled.hip",
+    "gemm_inst_bdirect_b.hip", "gemm_inst_grouped.hip",
     "gemm_inst_skinny.hip",
     "gemm_a4w4.hip", "mxfp4_format.hip",
 ]
@@ -47,6 +50,9 @@ HIP_FLAGS = [
 ]
 
 KERNEL_LIB = os.path.join(LIB, "libmbs_gemm_kernel.so")
+# The same kernels with the in-kernel phase timer compiled in (a measurement
+# tool: bench.py --phase-split and the sclk figure of the bench line).
+PHASE_LIB = os.path.join(LIB, "libmbs_gemm_phase.so")
 MODULE = os.path.join(LIB, "mbs_gemm_a4w4" + sysconfig.get_config_var("EXT_SUFFIX"))
 
 
@@ -57,22 +63,26 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"build step failed: {os.path.basename(cmd[0])} -> {cmd[-1]}")
 
 
-def _hip_object(src: str) -> str:
-    obj = os.path.join(LIB, "_obj", os.path.splitext(src)[0] + ".o")
+def _hip_object(src: str, phase_timer: bool = False) -> str:
+    sub = "_obj_phase" if phase_timer else "_obj"
+    obj = os.path.join(LIB, sub, os.path.splitext(src)[0] + ".o")
     os.makedirs(os.path.dirname(obj), exist_ok=True)
-    _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+    extra = ["-DMBS_PHASE_TIMER=1"] if phase_timer else []
+    _run([HIPCC, *HIP_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
     return obj
 
 
-def build_kernel_lib() -> str:
+def build_kernel_lib(phase_timer: bool = False) -> str:
+    """The C-ABI library; with phase_timer, its timer build (PHASE_LIB)."""
     os.makedirs(LIB, exist_ok=True)
+    out = PHASE_LIB if phase_timer else KERNEL_LIB
     workers = max(1, min(len(HIP_SOURCES), os.cpu_count() or 1, 16))
     with cf.ThreadPoolExecutor(max_workers=workers) as ex:
-        objs = list(ex.map(_hip_object, HIP_SOURCES))
-    tmp = KERNEL_LIB + ".tmp"
+        objs = list(ex.map(lambda src: _hip_object(src, phase_timer), HIP_SOURCES))
+    tmp = out + ".tmp"
     _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp])
-    os.replace(tmp, KERNEL_LIB)
-    return KERNEL_LIB
+    os.replace(tmp, out)
+    return out
 
 
 def build_module() -> str:
@@ -119,5 +129,8 @@ def build_all(with_oracle: bool = True) -> None:
 
 
 if __name__ == "__main__":
-    build_all()
-    print("built", KERNEL_LIB, MODULE)
+    if "--phase-timer" in sys.argv[1:]:
+        print("built", build_kernel_lib(phase_timer=True))
+    else:
+        build_all()
+        print("built", KERNEL_LIB, MODULE)

@@ -3,19 +3,17 @@
 //
 // Operand bytes follow the reference's contract (kernel/gemm_a4w4.h:5-26 of
 // the reference): plain row-major A [M,K/2], (16,16)-preshuffled B, shuffled
-// E8M0 scales.  Three kernel families:
+// E8M0 scales.  Kernel families (gemm_kernels.h):
 //
-//  * gemm_tiled_kernel  -- workgroup tile BM x BN, 4 (or fewer) waves.  A and
-//    B K-slices of 128 (one MFMA depth) are moved global->LDS by 16-byte
-//    buffer_load ... lds DMA into a 4-deep ring, prefetch distance 3.  The LDS
-//    image of each 16-row x 128-K fragment is exactly the MFMA operand order
-//    (lane L's 16 bytes at L*16), so every LDS read is a linear ds_read_b128
-//    with no bank conflicts.  For A the DMA lane->address map performs the
-//    row-major -> fragment reshuffle on the fly; preshuffled B is already in
-//    fragment order.  Scale dwords for each 256-K group ride the same DMA
-//    stream into a 2-slot ring.  The MFMA is issued with the operands swapped
-//    (B as src0) so each lane owns 4 consecutive n of one output row; the
-//    epilogue applies the MBS factors, packs bf16 (RNE) and stores 8 bytes.
+//  * gemm_bdirect_kernel -- persistent workgroups (one resident set per CU)
+//    loop over BM x BN tiles (x K-splits) in an XCD-aware order.  A moves
+//    global->LDS by 16-byte buffer_load ... lds DMA in 256-K pairs of whole
+//    cache lines, XOR-swizzled so the MFMA fragment reads are conflict-free;
+//    the preshuffled B is already in fragment order and loads straight into
+//    a VGPR ring.  The MFMA is issued with the operands swapped (B as src0)
+//    so each lane owns 4 consecutive n of one output row; the epilogue
+//    applies the MBS factors / alpha / bias, packs bf16 (RNE) and stores 16
+//    bytes per lane after two rounds of lane swaps.
 //  * gemm_skinny_kernel -- decode shapes (M <= 32): each wave streams 16 or
 //    32 rows of B (non-temporal) straight into VGPRs with a batch of its
 //    K-chunk in flight, reusing each A fragment for every B fragment; waves
@@ -33,10 +31,11 @@ namespace mbs {
 
 namespace {
 thread_local std::string g_last_error;
+// Phase-timer sums the persistent kernels add into (timer builds only).
+unsigned long long* g_phase = nullptr;
 }
 void set_last_error(const char* msg) { g_last_error = msg ? msg : ""; }
 
-MBS_TILED_SHAPES(MBS_TILED_EXTERN)
 MBS_BDIRECT_SHAPES_A(MBS_BDIRECT_EXTERN)
 MBS_BDIRECT_SHAPES_B(MBS_BDIRECT_EXTERN)
 MBS_BDIRECT_SHAPES_C(MBS_BDIRECT_EXTERN)
@@ -76,6 +75,33 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs p)
 }
 
 // ======================================================================
+// Expert-offset report of a grouped launch (one workgroup):
+//   status[0] = non-empty experts whose first row is not a multiple of 32
+//               (the grouped kernel skips them: their rows are not written),
+//   status[1] = offsets the kernel clamps: offsets[0] != 0, an entry outside
+//               [0, M], or a decrease offsets[e+1] < offsets[e].
+// ======================================================================
+__global__ void __launch_bounds__(256) check_groups_kernel(const int* off, int E, int M, uint32_t* status)
+{
+    __shared__ uint32_t cnt[2];
+    if (threadIdx.x < 2) cnt[threadIdx.x] = 0;
+    __syncthreads();
+    uint32_t unaligned = 0, clamped = 0;
+    for (int e = threadIdx.x; e <= E; e += 256) {
+        const int v = off[e];
+        clamped += (v < 0 || v > M || (e == 0 && v != 0) || (e < E && off[e + 1] < v)) ? 1u : 0u;
+        if (e < E) {
+            const int b = min(max(v, 0), M), end = min(max(off[e + 1], b), M);
+            unaligned += (end > b && (b & 31) != 0) ? 1u : 0u;
+        }
+    }
+    atomicAdd(&cnt[0], unaligned);
+    atomicAdd(&cnt[1], clamped);
+    __syncthreads();
+    if (threadIdx.x < 2) status[threadIdx.x] = cnt[threadIdx.x];
+}
+
+// ======================================================================
 // Host side: configurations, plans, launch
 // ======================================================================
 namespace {
@@ -86,49 +112,42 @@ int fail(int code, const std::string& msg)
     return code;
 }
 
-enum Family { kTiled = 0, kSkinny = 1 };
+enum Family { kPersistent = 0, kSkinny = 1 };
 
 struct Config {
     const char* name;
     Family family;
-    int bm, bn;        // tiled: workgroup tile; skinny: rows covered (16*MT) x B rows (16*NF)
+    int bm, bn;        // persistent: workgroup tile; skinny: rows covered (16*MT) x B rows (16*NF)
     int threads;
     int wgs_per_cu;    // resident workgroups per CU (LDS / register bound)
-    // Cost model constants.  Tiled: {us per 128-K stage with one workgroup
+    // Cost model constants.  Persistent: {us per 128-K stage with one workgroup
     // on the CU, us per stage with wgs_per_cu of them, us per work unit},
     // fitted to graph-replayed timings of every config and split count on 22
     // shapes on MI355X.  Skinny: {streaming efficiency, 0, 0}.
     struct {
         float a, b, c;
     } cost;
-    // launch(args, grid, general, split, stream); general: the K-tail variant
-    // (tiled kernels) or the dead-stage/K-tail variant (persistent kernels)
+    // launch(args, grid, general, split, stream); general: the dead-stage /
+    // K-tail variant
     hipError_t (*launch)(const GemmArgs&, dim3, bool, bool, hipStream_t);
     bool persistent = false;  // grid capped at the resident slots; workgroups loop over units
 };
 
 const Config kConfigs[] = {
-    {"tiled_256x256_w2x2", kTiled, 256, 256, 256, 1, {0.851f, 0.851f, 9.13f}, launch_tiled<T256x256>},
-    {"tiled_256x128_w2x2", kTiled, 256, 128, 256, 1, {0.572f, 0.572f, 3.72f}, launch_tiled<T256x128>},
-    {"tiled_128x256_w2x2", kTiled, 128, 256, 256, 1, {0.536f, 0.536f, 2.32f}, launch_tiled<T128x256>},
-    {"tiled_128x128_w2x2", kTiled, 128, 128, 256, 2, {0.283f, 0.566f, 3.53f}, launch_tiled<T128x128>},
-    {"tiled_64x256_w1x4", kTiled, 64, 256, 256, 2, {0.295f, 0.591f, 2.90f}, launch_tiled<T64x256>},
-    {"tiled_64x128_w1x2", kTiled, 64, 128, 128, 3, {0.209f, 0.530f, 3.58f}, launch_tiled<T64x128>},
-    {"tiled_64x64_w1x1", kTiled, 64, 64, 64, 4, {0.228f, 0.228f, 3.30f}, launch_tiled<T64x64>},
-    {"bdirect_256x256_w2x2", kTiled, 256, 256, 256, 1, {0.612f, 0.612f, 6.57f}, launch_bdirect<B256x256>, true},
-    {"bdirect_256x128_w2x2", kTiled, 256, 128, 256, 1, {0.389f, 0.389f, 3.09f}, launch_bdirect<B256x128>, true},
-    {"bdirect_128x256_w2x2", kTiled, 128, 256, 256, 1, {0.415f, 0.415f, 3.38f}, launch_bdirect<B128x256>, true},
-    {"bdirect_128x128_w2x2", kTiled, 128, 128, 256, 2, {0.235f, 0.446f, 2.54f}, launch_bdirect<B128x128>, true},
-    {"bdirect_64x256_w1x4", kTiled, 64, 256, 256, 2, {0.235f, 0.434f, 2.40f}, launch_bdirect<B64x256>, true},
-    {"bdirect_64x128_w1x2", kTiled, 64, 128, 128, 3, {0.191f, 0.357f, 1.96f}, launch_bdirect<B64x128>, true},
-    {"bdirect_64x64_w1x1", kTiled, 64, 64, 64, 4, {0.198f, 0.274f, 1.59f}, launch_bdirect<B64x64>, true},
-    {"bdirect_256x256_w1x4", kTiled, 256, 256, 256, 1, {0.611f, 0.611f, 7.01f}, launch_bdirect<B256x256w14>, true},
-    {"bdirect_256x128_w1x4", kTiled, 256, 128, 256, 1, {0.383f, 0.383f, 3.03f}, launch_bdirect<B256x128w14>, true},
-    {"bdirect_128x256_w1x4", kTiled, 128, 256, 256, 1, {0.367f, 0.367f, 3.14f}, launch_bdirect<B128x256w14>, true},
-    {"bdirect_192x256_w1x4", kTiled, 192, 256, 256, 1, {0.467f, 0.467f, 4.17f}, launch_bdirect<B192x256w14>, true},
-    {"bdirect_96x256_w1x4", kTiled, 96, 256, 256, 1, {0.333f, 0.333f, 2.77f}, launch_bdirect<B96x256w14>, true},
-    {"bdirect_64x512_w1x4", kTiled, 64, 512, 256, 1, {0.428f, 0.428f, 3.26f}, launch_bdirect<B64x512w14>, true},
-    {"bdirect_128x384_w1x4", kTiled, 128, 384, 256, 1, {0.455f, 0.455f, 4.55f}, launch_bdirect<B128x384w14>, true},
+    {"bdirect_256x256_w2x2", kPersistent, 256, 256, 256, 1, {0.612f, 0.612f, 6.57f}, launch_bdirect<B256x256>, true},
+    {"bdirect_256x128_w2x2", kPersistent, 256, 128, 256, 1, {0.389f, 0.389f, 3.09f}, launch_bdirect<B256x128>, true},
+    {"bdirect_128x256_w2x2", kPersistent, 128, 256, 256, 1, {0.415f, 0.415f, 3.38f}, launch_bdirect<B128x256>, true},
+    {"bdirect_128x128_w2x2", kPersistent, 128, 128, 256, 2, {0.235f, 0.446f, 2.54f}, launch_bdirect<B128x128>, true},
+    {"bdirect_64x256_w1x4", kPersistent, 64, 256, 256, 2, {0.235f, 0.434f, 2.40f}, launch_bdirect<B64x256>, true},
+    {"bdirect_64x128_w1x2", kPersistent, 64, 128, 128, 3, {0.191f, 0.357f, 1.96f}, launch_bdirect<B64x128>, true},
+    {"bdirect_64x64_w1x1", kPersistent, 64, 64, 64, 4, {0.198f, 0.274f, 1.59f}, launch_bdirect<B64x64>, true},
+    {"bdirect_256x256_w1x4", kPersistent, 256, 256, 256, 1, {0.611f, 0.611f, 7.01f}, launch_bdirect<B256x256w14>, true},
+    {"bdirect_256x128_w1x4", kPersistent, 256, 128, 256, 1, {0.383f, 0.383f, 3.03f}, launch_bdirect<B256x128w14>, true},
+    {"bdirect_128x256_w1x4", kPersistent, 128, 256, 256, 1, {0.367f, 0.367f, 3.14f}, launch_bdirect<B128x256w14>, true},
+    {"bdirect_192x256_w1x4", kPersistent, 192, 256, 256, 1, {0.467f, 0.467f, 4.17f}, launch_bdirect<B192x256w14>, true},
+    {"bdirect_96x256_w1x4", kPersistent, 96, 256, 256, 1, {0.333f, 0.333f, 2.77f}, launch_bdirect<B96x256w14>, true},
+    {"bdirect_64x512_w1x4", kPersistent, 64, 512, 256, 1, {0.428f, 0.428f, 3.26f}, launch_bdirect<B64x512w14>, true},
+    {"bdirect_128x384_w1x4", kPersistent, 128, 384, 256, 1, {0.455f, 0.455f, 4.55f}, launch_bdirect<B128x384w14>, true},
     // skinny: bm = rows covered (16*MT), bn = B rows per workgroup (16*NF)
     // eff = streaming efficiency relative to the best variant (cold N=K=8192 timings)
     {"skinny_m16_n32_w16", kSkinny, 16, 32, 1024, 1, {0.94f, 0.f, 0.f}, launch_skinny<1, 2, 16, 4>},
@@ -218,7 +237,7 @@ bool make_plan(int config, int want_splits, int M, int N, int K, Plan* out)
 }
 
 // Cost model: estimated time of a plan in ns, including the launch.
-// Tiled kernels: rounds x (stages x stage time + per-unit time), where the
+// Persistent kernels: rounds x (stages x stage time + per-unit time), where the
 // stage time grows from cost.a (one workgroup per CU) to cost.b (wgs_per_cu
 // of them); split-K adds the fp32 partial round trip (the reduce kernel).
 // The constants were fitted to measured times (log-error least squares).
@@ -253,7 +272,7 @@ double plan_cost(const Plan& pl, int M, int N, int K)
         c.wgs_per_cu == 1 ? c.cost.a
                           : c.cost.a + (c.cost.b - c.cost.a) * (per_cu - 1) / (c.wgs_per_cu - 1);
     const int stages = c.persistent ? (pl.sps + 3) / 4 * 4 : pl.sps;
-    // Decode-sized M: a tiled kernel streams B only two stages ahead and
+    // Decode-sized M: a persistent kernel streams B only a few stages ahead and
     // leaves most MFMA rows empty; its HBM floor is taken at 60%.
     const double floor_ns = M <= 32 ? hbm_ns / 0.6 : hbm_ns;
     return kLaunchNs + std::max(rounds * (stages * stage_us + c.cost.c) * 1000.0, floor_ns) +
@@ -336,6 +355,8 @@ bool choose_plan(int M, int N, int K, size_t ws_avail, Plan* best)
     return have;
 }
 
+bool misaligned(const void* p, uintptr_t a) { return p && reinterpret_cast<uintptr_t>(p) % a != 0; }
+
 int validate(const uint8_t* A, const uint8_t* B, const uint8_t* As, const uint8_t* Bs,
              const uint8_t* Af, const uint8_t* Bf, void* out, int M, int N, int K, int Mpad,
              int snp)
@@ -346,6 +367,14 @@ int validate(const uint8_t* A, const uint8_t* B, const uint8_t* As, const uint8_
         return fail(MBS_ERR_ARGUMENT, "null operand pointer");
     if ((Af == nullptr) != (Bf == nullptr) && M > 0)
         return fail(MBS_ERR_ARGUMENT, "AFactor and BFactor must be given together");
+    // The kernels move A, B, the scales and the output in 16-byte units and
+    // the factor bytes in dwords (buffer loads and LDS DMA at offsets that
+    // are multiples of those sizes from each base).
+    if (misaligned(A, 16) || misaligned(B, 16) || misaligned(As, 16) || misaligned(Bs, 16) ||
+        misaligned(out, 16))
+        return fail(MBS_ERR_ARGUMENT, "A, B, AScale, BScale and out must be 16-byte aligned");
+    if (misaligned(Af, 4) || misaligned(Bf, 4))
+        return fail(MBS_ERR_ARGUMENT, "AFactor and BFactor must be 4-byte aligned");
     if (M < 0 || N < 16 || K < 64)
         return fail(MBS_ERR_ARGUMENT, "need M >= 0, N >= 16, K >= 64; got M=" + std::to_string(M) +
                                           " N=" + std::to_string(N) + " K=" + std::to_string(K));
@@ -377,6 +406,8 @@ int run_plan(const Plan& pl, const uint8_t* A, const uint8_t* B, const uint8_t* 
     if (pl.ws_bytes > ws_bytes || (pl.ws_bytes && !ws))
         return fail(MBS_ERR_WORKSPACE, "workspace too small: need " + std::to_string(pl.ws_bytes) +
                                            " bytes");
+    if (pl.ws_bytes && misaligned(ws, 16)) return fail(MBS_ERR_ARGUMENT, "workspace must be 16-byte aligned");
+    if (misaligned(bias, 16)) return fail(MBS_ERR_ARGUMENT, "bias must be 16-byte aligned");
     GemmArgs a{};
     a.A = A; a.B = B; a.As = As; a.Bs = Bs; a.Af = Af; a.Bf = Bf;
     a.out = static_cast<uint16_t*>(out);
@@ -388,6 +419,7 @@ int run_plan(const Plan& pl, const uint8_t* A, const uint8_t* B, const uint8_t* 
     a.sps = pl.sps;
     a.alpha = alpha;
     a.bias = static_cast<const uint16_t*>(bias);
+    a.phase = g_phase;
     hipStream_t s = static_cast<hipStream_t>(stream);
     (void)hipGetLastError();  // do not report a stale error as ours
     // Persistent kernels take their general variant when a unit can have
@@ -487,6 +519,7 @@ int run_grouped(int g, const uint8_t* A, const uint8_t* B, const uint8_t* As, co
     a.n_groups = E;
     a.alpha = alpha;
     a.bias = static_cast<const uint16_t*>(bias);
+    a.phase = g_phase;
     const int S_total = stages_of(K);
     const bool gen = (K % 128) != 0 || a.sps % 4 != 0 || S_total % a.sps != 0;
     const int units = grouped_units_bound(c, M, N, E);
@@ -572,10 +605,30 @@ int mbs_gemm_a4w4_grouped_launch_ex(const uint8_t* A, const uint8_t* B, const ui
     if (config < -1 || config >= kNumGrouped)
         return fail(MBS_ERR_CONFIG, "grouped config out of range");
     if (!(alpha == alpha)) return fail(MBS_ERR_ARGUMENT, "alpha is NaN");
+    if (misaligned(group_offsets, 4)) return fail(MBS_ERR_ARGUMENT, "group_offsets must be 4-byte aligned");
+    if (misaligned(bias, 16)) return fail(MBS_ERR_ARGUMENT, "bias must be 16-byte aligned");
     if (M == 0) return MBS_OK;
     const int g = config >= 0 ? config : choose_grouped(M, N, K, num_groups);
     return run_grouped(g, A, B, AScale, BScale, AFactor, BFactor, group_offsets, num_groups, out, M,
                        N, K, scaleN_pad, stream, alpha, bias);
+}
+
+int mbs_gemm_a4w4_check_groups(const int* group_offsets, int num_groups, int M, uint32_t* status,
+                               void* stream)
+{
+    set_last_error("");
+    if (!group_offsets || !status) return fail(MBS_ERR_ARGUMENT, "null group_offsets or status");
+    if (num_groups < 1 || num_groups > kMaxGroups)
+        return fail(MBS_ERR_ARGUMENT, "num_groups must be in [1, " + std::to_string(kMaxGroups) + "]");
+    if (M < 0) return fail(MBS_ERR_ARGUMENT, "M must be >= 0");
+    if (reinterpret_cast<uintptr_t>(group_offsets) % 4 || reinterpret_cast<uintptr_t>(status) % 4)
+        return fail(MBS_ERR_ARGUMENT, "group_offsets and status must be 4-byte aligned");
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(check_groups_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       group_offsets, num_groups, M, status);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(MBS_ERR_LAUNCH, std::string("launch failed: ") + hipGetErrorString(e));
+    return MBS_OK;
 }
 
 int mbs_gemm_a4w4_grouped_num_configs(void) { return kNumGrouped; }
@@ -654,5 +707,14 @@ int mbs_gemm_a4w4_launch_ex(int config, int splits, const uint8_t* A, const uint
     return run_plan(pl, A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, scaleN_pad,
                     workspace, workspace_bytes, stream, alpha, bias);
 }
+
+#if MBS_PHASE_TIMER
+// Timer builds (libmbs_gemm_phase.so) only: every later persistent-kernel
+// launch adds its phase sums into `sums` (kPhSlots device words per
+// workgroup, 1024 workgroups at most, cleared by
+// the caller); nullptr detaches.
+void mbs_phase_timer_attach(unsigned long long* sums) { g_phase = sums; }
+int mbs_phase_timer_slots(void) { return kPhSlots; }
+#endif
 
 }  // extern "C"

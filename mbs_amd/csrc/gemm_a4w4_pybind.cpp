@@ -35,7 +35,21 @@ void check_status(int st, const char* what)
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 int64_t scale_pad(int64_t K) { return round_up((K + 31) / 32, 8); }
 
-at::Tensor as_bytes(const at::Tensor& t) { return t.view(at::kByte).contiguous(); }
+// A contiguous byte view of t.  The kernels need 16-byte aligned operands
+// (4-byte for the factor bytes); a view starting elsewhere in its storage is
+// copied into a fresh (aligned) allocation instead of being refused.
+at::Tensor as_bytes(const at::Tensor& t, uintptr_t align = 16)
+{
+    at::Tensor b = t.view(at::kByte).contiguous();
+    if (reinterpret_cast<uintptr_t>(b.data_ptr()) % align) b = b.clone();
+    return b;
+}
+at::Tensor aligned_contiguous(const at::Tensor& t)
+{
+    at::Tensor c = t.contiguous();
+    if (reinterpret_cast<uintptr_t>(c.data_ptr()) % 16) c = c.clone();
+    return c;
+}
 
 struct Operands {
     at::Tensor A, B, As, Bs, Af, Bf;
@@ -84,8 +98,8 @@ Operands prepare(const at::Tensor& A, const at::Tensor& B, const at::Tensor& A_s
     TORCH_CHECK(has_a == has_b, "gemm_a4w4: A_factor and B_factor must be given together");
     o.factors = has_a;
     if (o.factors) {
-        o.Af = as_bytes(*A_factor);
-        o.Bf = as_bytes(*B_factor);
+        o.Af = as_bytes(*A_factor, 4);
+        o.Bf = as_bytes(*B_factor, 4);
         TORCH_CHECK(o.Af.is_cuda() && o.Af.numel() == o.M, "gemm_a4w4: A_factor must hold M = ",
                     o.M, " bytes on device, got ", o.Af.numel());
         TORCH_CHECK(o.Bf.is_cuda() && o.Bf.numel() == o.N, "gemm_a4w4: B_factor must hold N = ",
@@ -115,7 +129,7 @@ at::Tensor run(const Operands& o, int config, int splits, double alpha = 1.0,
         TORCH_CHECK(bias->is_cuda() && bias->device() == o.A.device() &&
                         bias->scalar_type() == at::kBFloat16 && bias->numel() == o.N,
                     "gemm_a4w4: bias must be a bf16 device tensor of N entries");
-        bu = bias->contiguous();
+        bu = aligned_contiguous(*bias);
     }
     if (alpha != 1.0 || bu.defined())
         st = mbs_gemm_a4w4_launch_ex(config, splits, o.A.data_ptr<uint8_t>(),
@@ -169,7 +183,7 @@ std::tuple<at::Tensor, at::Tensor> quantize_mxfp4(at::Tensor x, bool shuffle, in
 {
     TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.scalar_type() == at::kBFloat16,
                 "quantize_mxfp4: x must be a 2D bf16 device tensor");
-    auto xc = x.contiguous();
+    auto xc = aligned_contiguous(x);
     const int64_t R = xc.size(0), K = xc.size(1);
     TORCH_CHECK(K % 32 == 0, "quantize_mxfp4: K must be a multiple of 32");
     c10::DeviceGuard guard(x.device());
@@ -192,7 +206,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> quantize_mxfp4_mbs(at::Tensor x, 
 {
     TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.scalar_type() == at::kBFloat16,
                 "quantize_mxfp4_mbs: x must be a 2D bf16 device tensor");
-    auto xc = x.contiguous();
+    auto xc = aligned_contiguous(x);
     const int64_t R = xc.size(0), K = xc.size(1);
     TORCH_CHECK(K % 32 == 0, "quantize_mxfp4_mbs: K must be a multiple of 32");
     c10::DeviceGuard guard(x.device());
@@ -310,15 +324,35 @@ at::Tensor dequant_mxfp4(at::Tensor packed, at::Tensor scale_shuffled, bool b_pr
     return out;
 }
 
+// (non-empty experts starting off a 32-row boundary, clamped offsets) of a
+// device offset vector of E+1 entries (mbs_gemm_a4w4_check_groups;
+// synchronises the stream).
+std::tuple<int64_t, int64_t> check_groups(at::Tensor group_offsets, int64_t M)
+{
+    TORCH_CHECK(group_offsets.is_cuda() && group_offsets.dim() == 1 && group_offsets.numel() >= 2 &&
+                    group_offsets.scalar_type() == at::kInt,
+                "check_groups: group_offsets must be an int32 device vector of E+1 entries");
+    auto g = aligned_contiguous(group_offsets);
+    c10::DeviceGuard guard(g.device());
+    auto st = torch::empty({2}, torch::TensorOptions().dtype(torch::kInt32).device(g.device()));
+    check_status(mbs_gemm_a4w4_check_groups(g.data_ptr<int32_t>(), (int)(g.numel() - 1), (int)M,
+                                            reinterpret_cast<uint32_t*>(st.data_ptr<int32_t>()),
+                                            current_stream(g)),
+                 "check_groups");
+    auto h = st.cpu();
+    return {(int64_t)(uint32_t)h[0].item<int32_t>(), (int64_t)(uint32_t)h[1].item<int32_t>()};
+}
+
 // Grouped (MoE) GEMM: out[rows of expert e] = A[rows] @ B[e]^T (see
 // mbs_gemm_a4w4_grouped_launch).  B: [E, N, K/2] or [E*N, K/2] bytes,
 // B_scale: E shuffled blocks, group_offsets: int32 [E+1] (a host tensor is
 // checked -- 0 first, non-decreasing multiples of 32, last <= M -- and
-// copied to the device; a device tensor is used as it is).
+// copied to the device; a device tensor is used as it is, or checked on the
+// device first with validate=True).
 at::Tensor gemm_a4w4_grouped(at::Tensor A, at::Tensor B, at::Tensor A_scale, at::Tensor B_scale,
                              at::Tensor group_offsets, c10::optional<at::Tensor> A_factor,
                              c10::optional<at::Tensor> B_factor, int64_t config, double alpha,
-                             c10::optional<at::Tensor> bias)
+                             c10::optional<at::Tensor> bias, bool validate)
 {
     TORCH_CHECK(group_offsets.dim() == 1 && group_offsets.numel() >= 2 &&
                     group_offsets.scalar_type() == at::kInt,
@@ -348,20 +382,28 @@ at::Tensor gemm_a4w4_grouped(at::Tensor A, at::Tensor B, at::Tensor A_scale, at:
         goff = g.to(A.device());
     } else {
         TORCH_CHECK(goff.device() == A.device(), "gemm_a4w4_grouped: group_offsets on another device");
-        goff = goff.contiguous();
+        goff = aligned_contiguous(goff);
+        if (validate) {
+            // Device offsets are read by the kernel unchecked; on request,
+            // check them on the device first (synchronises the stream).
+            const auto st = check_groups(goff, M);
+            TORCH_CHECK(std::get<0>(st) == 0 && std::get<1>(st) == 0, "gemm_a4w4_grouped: ",
+                        std::get<0>(st), " experts start at a row that is not a multiple of 32 and ",
+                        std::get<1>(st), " offsets lie outside [0, M] or decrease");
+        }
     }
     c10::DeviceGuard guard(A.device());
     auto Au = as_bytes(A), Bu = as_bytes(B), Asu = as_bytes(A_scale), Bsu = as_bytes(B_scale);
     at::Tensor Af, Bf;
     if (A_factor.has_value()) {
-        Af = as_bytes(*A_factor);
-        Bf = as_bytes(*B_factor);
+        Af = as_bytes(*A_factor, 4);
+        Bf = as_bytes(*B_factor, 4);
         TORCH_CHECK(Af.is_cuda() && Bf.is_cuda() && Af.numel() == M && Bf.numel() == E * N,
                     "gemm_a4w4_grouped: factors must be device bytes of M and E*N entries");
     }
     at::Tensor bz;
     if (bias.has_value()) {
-        bz = bias->contiguous();
+        bz = aligned_contiguous(*bias);
         TORCH_CHECK(bz.is_cuda() && bz.device() == A.device() && bz.scalar_type() == at::kBFloat16 &&
                         bz.numel() == E * N,
                     "gemm_a4w4_grouped: bias must be a bf16 device tensor of E*N entries");
@@ -423,7 +465,10 @@ PYBIND11_MODULE(mbs_gemm_a4w4, m)
           pybind11::arg("B_scale"), pybind11::arg("group_offsets"),
           pybind11::arg("A_factor") = pybind11::none(), pybind11::arg("B_factor") = pybind11::none(),
           pybind11::arg("config") = -1, pybind11::arg("alpha") = 1.0,
-          pybind11::arg("bias") = pybind11::none());
+          pybind11::arg("bias") = pybind11::none(), pybind11::arg("validate") = false);
+    m.def("check_groups", &check_groups,
+          "(experts starting off a 32-row boundary, clamped offsets) of device group offsets",
+          pybind11::arg("group_offsets"), pybind11::arg("M"));
     m.def("grouped_num_configs", []() { return mbs_gemm_a4w4_grouped_num_configs(); });
     m.def("grouped_config_name",
           [](int64_t c) { return std::string(mbs_gemm_a4w4_grouped_config_name((int)c)); });

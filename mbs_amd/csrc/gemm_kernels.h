@@ -39,9 +39,81 @@ struct GemmArgs {
     // no bias leave the plain product.  bias: bf16 [N] (grouped: [E][N]) or null.
     float alpha;
     const uint16_t* bias;
+    // Phase-timer sums (kPhSlots words; timer builds only, else null).
+    unsigned long long* phase;
 };
 // Most experts a grouped launch takes (the per-expert tile table lives in LDS).
 constexpr int kMaxGroups = 1024;
+
+// ---------------------------------------------------------------------------
+// Phase timer of the persistent kernel (built only with MBS_PHASE_TIMER=1,
+// into a separate library; the product build compiles every call below to
+// nothing).  Each wave stamps the shader clock (s_memtime) at the phase
+// boundaries of its loop and sums the intervals per phase in SGPRs; at the
+// end lane 0 adds them into GemmArgs::phase with vector atomics:
+//   [kPhPro]   kernel start -> first stage,
+//   [kPhWait]  stage-top vmcnt waits (and the one before each epilogue),
+//   [kPhBar]   the workgroup barriers that follow them,
+//   [kPhBody]  stage bodies: MFMAs, LDS reads and the loads they issue,
+//   [kPhEpi]   MFMA drain and epilogue (conversion, lane swaps, stores),
+//   [kPhNext]  the next unit's set-up (factor and bias DMAs, unit and
+//              offset arithmetic) up to its first stage,
+//   [kPhStages], [kPhUnits]  stage and unit counts,
+// (per workgroup: GemmArgs::phase holds gridDim.x x kPhSlots words)
+//   [kPhClk], [kPhRt]  s_memtime and s_memrealtime (100 MHz) ticks of the
+//              whole kernel, wave 0 of each workgroup: their ratio is the
+//              shader clock the kernel ran at.
+// The stamps' s_waitcnt lgkmcnt(0) also waits for the look-ahead LDS reads
+// in flight at a stage top, so the timed kernel runs slightly slower.
+#ifndef MBS_PHASE_TIMER
+#define MBS_PHASE_TIMER 0
+#endif
+enum PhaseSlot { kPhPro = 0, kPhWait, kPhBar, kPhBody, kPhEpi, kPhNext, kPhStages, kPhUnits, kPhClk, kPhRt, kPhSlots };
+
+struct PhaseClock {
+#if MBS_PHASE_TIMER
+    uint64_t last = 0, t0 = 0, r0 = 0;
+    uint64_t acc[kPhStages] = {};
+    uint32_t stages = 0, units = 0;
+    __device__ __forceinline__ void start()
+    {
+        r0 = __builtin_amdgcn_s_memrealtime();
+        t0 = last = __builtin_amdgcn_s_memtime();
+    }
+    // The time since the previous stamp goes to phase `ph`.
+    __device__ __forceinline__ void mark(int ph)
+    {
+        const uint64_t t = __builtin_amdgcn_s_memtime();
+        const uint64_t d = t - last;
+        last = t;
+        static_for<kPhStages>([&](auto P) { acc[P] += (P == ph) ? d : 0; });
+    }
+    __device__ __forceinline__ void stage() { ++stages; }
+    __device__ __forceinline__ void unit() { ++units; }
+    // Each workgroup adds into its own kPhSlots words (out + blockIdx.x *
+    // kPhSlots): only its waves contend for them.
+    __device__ __forceinline__ void flush(unsigned long long* out)
+    {
+        const uint64_t t1 = __builtin_amdgcn_s_memtime();
+        const uint64_t r1 = __builtin_amdgcn_s_memrealtime();
+        if (!out || (threadIdx.x & 63) != 0) return;
+        out += (size_t)blockIdx.x * kPhSlots;
+        static_for<kPhStages>([&](auto P) { atomicAdd(out + P, (unsigned long long)acc[P]); });
+        atomicAdd(out + kPhStages, (unsigned long long)stages);
+        atomicAdd(out + kPhUnits, (unsigned long long)units);
+        if (threadIdx.x == 0) {
+            atomicAdd(out + kPhClk, (unsigned long long)(t1 - t0));
+            atomicAdd(out + kPhRt, (unsigned long long)(r1 - r0));
+        }
+    }
+#else
+    __device__ __forceinline__ void start() {}
+    __device__ __forceinline__ void mark(int) {}
+    __device__ __forceinline__ void stage() {}
+    __device__ __forceinline__ void unit() {}
+    __device__ __forceinline__ void flush(unsigned long long*) {}
+#endif
+};
 
 // Whether the bf16 epilogue has anything beyond the plain conversion.
 inline bool affine_epilogue(const GemmArgs& a)
@@ -50,312 +122,10 @@ inline bool affine_epilogue(const GemmArgs& a)
 }
 
 // ======================================================================
-// Tiled kernel
+// B-direct persistent kernel
 // ======================================================================
-template <int BM_, int BN_, int WGM_, int WGN_>
-struct TileShape {
-    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
-    static constexpr int NW = WGM * WGN, NT = 64 * NW;
-    static constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile
-    static constexpr int FM = WM / 16, FN = WN / 16;    // 16x16 fragments per wave
-    static constexpr int AF = BM / 16, BF = BN / 16;    // 1-KiB fragments per stage
-    static constexpr int DA = AF / NW, DB = BF / NW;    // data DMAs per wave per stage
-    static constexpr int SGA = BM / 32, SGB = BN / 32;  // 256-B scale groups per 256 K
-    static constexpr int DS = (SGA + SGB + NW - 1) / NW;  // scale DMAs per wave per group
-    static constexpr int SA = FM / 2, SB = FN / 2;      // scale dwords per wave per group
-    static constexpr int STAGE = (AF + BF) * 1024;
-    static constexpr int SCB = DS * NW * 256;
-    static constexpr int NBUF = 4, PF = 3;
-    static_assert(AF % NW == 0 && BF % NW == 0, "fragments must split evenly over waves");
-    static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
-    static_assert(NBUF * STAGE + 2 * SCB <= 160 * 1024, "LDS budget");
-};
-
-template <class T, bool KTAIL, bool SPLIT>
-__global__ void __launch_bounds__(T::NT) gemm_tiled_kernel(const GemmArgs p)
-{
-    // One __shared__ object per ring slot: the compiler tracks in-flight LDS
-    // DMA per LDS object (alias scopes), so distinct objects let it see that
-    // reading slot s does not wait on the DMA into slot s+1..s+3.
-    __shared__ __attribute__((aligned(1024))) uint8_t sd0[T::STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t sd1[T::STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t sd2[T::STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t sd3[T::STAGE];
-    __shared__ __attribute__((aligned(256))) uint8_t ss0[T::SCB];
-    __shared__ __attribute__((aligned(256))) uint8_t ss1[T::SCB];
-    auto sdata = [&](auto B) __attribute__((always_inline)) -> uint8_t* {
-        constexpr int b = decltype(B)::value;
-        if constexpr (b == 0) return sd0;
-        else if constexpr (b == 1) return sd1;
-        else if constexpr (b == 2) return sd2;
-        else return sd3;
-    };
-    auto sscale = [&](auto S) __attribute__((always_inline)) -> uint8_t* {
-        if constexpr (decltype(S)::value == 0) return ss0;
-        else return ss1;
-    };
-
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = w / T::WGN, wn = w % T::WGN;
-
-    // ---- tile / split assignment: XCD-aware, grouped along M -----------
-    // Workgroups are dealt round-robin over the 8 XCDs; renumber so that
-    // consecutive logical ids share an XCD (and its L2), then walk tiles in
-    // groups of 8 tile-rows so concurrently running tiles share A and B.
-    int bid = blockIdx.x;
-    const int G = gridDim.x;
-    if ((G & 7) == 0) bid = (bid & 7) * (G >> 3) + (bid >> 3);
-    const int tiles = p.tiles_m * p.tiles_n;
-    const int split = bid / tiles;
-    const int t = bid - split * tiles;
-    constexpr int GROUP = 8;
-    const int grp = t / (GROUP * p.tiles_n);
-    const int first_m = grp * GROUP;
-    const int gsz = min(p.tiles_m - first_m, GROUP);
-    const int tin = t - grp * GROUP * p.tiles_n;
-    const int m0 = (first_m + tin % gsz) * T::BM;
-    const int n0 = (tin / gsz) * T::BN;
-
-    const int K = p.K, Kp = K >> 1;
-    const int S_total = (K + 127) >> 7;
-    const int s_begin = split * p.sps;
-    const int n_st = min(p.sps, S_total - s_begin);
-
-    // ---- buffer resources (tile-based so offsets stay small) -----------
-    const int rows_a = min(T::BM, p.M - m0);
-    const int rows_b = min(T::BN, p.N - n0);
-    const int Mpad = (p.M + 31) & ~31, Npad = (p.N + 31) & ~31;
-    const rsrc_t rA = make_rsrc(p.A + (size_t)m0 * Kp, (uint32_t)(rows_a * Kp));
-    const rsrc_t rB = make_rsrc(p.B + (size_t)(n0 >> 4) * K * 8, (uint32_t)(rows_b * Kp));
-    const rsrc_t rAs = make_rsrc(p.As + (size_t)(m0 >> 5) * 32 * p.snp,
-                                 (uint32_t)(min(T::BM, Mpad - m0) * p.snp));
-    const rsrc_t rBs = make_rsrc(p.Bs + (size_t)(n0 >> 5) * 32 * p.snp,
-                                 (uint32_t)(min(T::BN, Npad - n0) * p.snp));
-
-    // ---- per-lane DMA offsets ------------------------------------------
-    // A fragment f, lane i: row 16f + i%16, K-block i/16 of the stage.
-    // B fragment f, lane i: preshuffled, 16 contiguous bytes at i*16.
-    uint32_t voA[T::DA], voB[T::DB];
-    static_for<T::DA>([&](auto d) {
-        const int fa = w * T::DA + d;
-        voA[d] = (uint32_t)((16 * fa + (lane & 15)) * Kp + (lane >> 4) * 16);
-    });
-    static_for<T::DB>([&](auto d) {
-        const int fb = w * T::DB + d;
-        voB[d] = (uint32_t)(fb * K * 8 + lane * 16);
-    });
-    const bool hi_lane = lane >= 32;  // K-blocks 2,3 of a 128-K stage
-    const uint32_t hi_bit = hi_lane ? kOOB : 0u;
-
-    // ---- DMA items ---------------------------------------------------------
-    // One stage's DMA group: DA fragments of A, DB of B and, on the first
-    // stage of a 256-K group, DS scale groups.  Stages past the split's end
-    // are still issued, with every lane out of range: they write zeros into a
-    // free slot and keep the per-stage VMEM count uniform, which the vmcnt
-    // bookkeeping relies on.  The out-of-range bit is OR-ed in rather than
-    // selected: a select on a wave-uniform condition gets turned into a
-    // branch that would split the pipelined loop body.
-    auto dead_bits = [&](int ls) __attribute__((always_inline)) {
-        const int s = s_begin + ls;
-        uint32_t dead = (uint32_t)(ls >= n_st) << 31;
-        if (KTAIL) dead |= ((uint32_t)(s == S_total - 1) << 31) & hi_bit;
-        asm volatile("" : "+v"(dead));
-        return dead;
-    };
-    auto issue_item = [&](auto BUF, auto D, int ls, uint32_t dead) __attribute__((always_inline)) {
-        constexpr int d = decltype(D)::value;
-        const int s = s_begin + ls;
-        if constexpr (d < T::DA) {
-            dma16(rA, sdata(BUF) + (w * T::DA + d) * 1024, (voA[d] + (uint32_t)s * 64u) | dead);
-        } else if constexpr (d < T::DA + T::DB) {
-            constexpr int e = d - T::DA;
-            dma16(rB, sdata(BUF) + (T::AF + w * T::DB + e) * 1024,
-                  (voB[e] + (uint32_t)s * 1024u) | dead);
-        } else {
-            constexpr int e = d - T::DA - T::DB;
-            constexpr int slot = (decltype(BUF)::value >> 1) & 1;
-            const int q = w * T::DS + e;
-            const bool is_a = q < T::SGA;
-            const bool is_b = !is_a && q < T::SGA + T::SGB;
-            const uint32_t g = (uint32_t)(s >> 1) * 256u + lane * 4;
-            const uint32_t qdead = ((uint32_t)(ls >= n_st) | (uint32_t)!(is_a || is_b)) << 31;
-            const uint32_t base = (uint32_t)((is_a ? q : q - T::SGA) * 32 * p.snp);
-            dma4(is_a ? rAs : rBs, sscale(std::integral_constant<int, slot>{}) + q * 256,
-                 (base + g) | qdead);
-        }
-    };
-    // VMEM ops one wave issues per local stage (static parity).
-    constexpr int CNT_ODD = T::DA + T::DB;
-    constexpr int CNT_EVEN = T::DA + T::DB + T::DS;
-
-    i32x4 ra[2][T::FM], rb[2][T::FN];
-    int sa[2][T::SA], sb[2][T::SB];
-    f32x4 acc[T::FM][T::FN];
-    static_for<T::FM>([&](auto i) {
-        static_for<T::FN>([&](auto j) { acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f}; });
-    });
-
-    // ---- LDS read items: stage in slot BUF -> register set R ----------------
-    auto read_item = [&](auto BUF, auto R, auto X) __attribute__((always_inline)) {
-        constexpr int r = decltype(R)::value;
-        constexpr int x = decltype(X)::value;
-        constexpr int slot = (decltype(BUF)::value >> 1) & 1;
-        if constexpr (x < T::FM) {
-            ra[r][x] = *reinterpret_cast<const i32x4*>(sdata(BUF) + (wm * T::FM + x) * 1024 +
-                                                       lane * 16);
-        } else if constexpr (x < T::FM + T::FN) {
-            constexpr int j = x - T::FM;
-            rb[r][j] = *reinterpret_cast<const i32x4*>(
-                sdata(BUF) + (T::AF + wn * T::FN + j) * 1024 + lane * 16);
-        } else if constexpr (x < T::FM + T::FN + T::SA) {
-            constexpr int i = x - T::FM - T::FN;
-            sa[slot][i] = *reinterpret_cast<const int*>(
-                sscale(std::integral_constant<int, slot>{}) + ((wm * T::WM) / 32 + i) * 256 +
-                lane * 4);
-        } else {
-            constexpr int j = x - T::FM - T::FN - T::SA;
-            sb[slot][j] = *reinterpret_cast<const int*>(
-                sscale(std::integral_constant<int, slot>{}) +
-                (T::SGA + (wn * T::WN) / 32 + j) * 256 + lane * 4);
-        }
-    };
-    auto read_all = [&](auto BUF, auto R) __attribute__((always_inline)) {
-        constexpr int NX = T::FM + T::FN + (((decltype(BUF)::value & 1) == 0) ? T::SA + T::SB : 0);
-        static_for<NX>([&](auto X) { read_item(BUF, R, X); });
-    };
-
-    // ---- one pipelined stage ----------------------------------------------
-    // Compute stage ls (slot u, registers u&1) while issuing the DMA group of
-    // stage ls+3 and the LDS reads of stage ls+1.  The work is cut into FM
-    // chunks (one A-fragment row of FN MFMAs each) and each chunk carries an
-    // even share of the DMAs and LDS reads; sched_barrier(0) between chunks
-    // keeps the compiler from clustering the reads behind the MFMAs.
-    auto stage = [&](auto U, int ls) __attribute__((always_inline)) {
-        constexpr int u = decltype(U)::value;
-        constexpr int r = u & 1, slot = (u >> 1) & 1, h = u & 1;
-        using BUFN = std::integral_constant<int, (u + 1) & 3>;  // slot read now
-        using BUFD = std::integral_constant<int, (u + 3) & 3>;  // slot refilled now
-        using RN = std::integral_constant<int, (u + 1) & 1>;
-        constexpr int NDMA = T::DA + T::DB + ((((u + 3) & 1) == 0) ? T::DS : 0);
-        constexpr int NRD = T::FM + T::FN + ((((u + 1) & 1) == 0) ? T::SA + T::SB : 0);
-        constexpr int NCH = T::FM;
-
-        // stage ls+1 must have landed for every wave; ls+2 may be in flight
-        wait_vmcnt<((u & 1) == 0) ? CNT_EVEN : CNT_ODD>();
-        barrier();
-        __builtin_amdgcn_sched_barrier(0);
-
-        const uint32_t dead = dead_bits(ls + 3);
-        int sav[T::SA], sbv[T::SB];
-        static_for<T::SA>([&](auto i) { sav[i] = sa[slot][i]; });
-        static_for<T::SB>([&](auto j) { sbv[j] = sb[slot][j]; });
-        if constexpr (KTAIL) {
-            // Blocks past K (zeroed data) get a finite scale so 0 * scale
-            // cannot become NaN when the caller's padding bytes are 0xFF.
-            const bool tail = (s_begin + ls == S_total - 1) && hi_lane;
-            static_for<T::SA>([&](auto i) { sav[i] = tail ? 0x7F7F7F7F : sav[i]; });
-            static_for<T::SB>([&](auto j) { sbv[j] = tail ? 0x7F7F7F7F : sbv[j]; });
-        }
-        static_for<NCH>([&](auto C) {
-            constexpr int c = decltype(C)::value;
-            static_for<NDMA>([&](auto D) {
-                if constexpr (D * NCH / NDMA == c) issue_item(BUFD{}, D, ls + 3, dead);
-            });
-            static_for<NRD>([&](auto X) {
-                if constexpr (X * NCH / NRD == c) read_item(BUFN{}, RN{}, X);
-            });
-            static_for<T::FN>([&](auto j) {
-                constexpr int opb = (j & 1) + 2 * h;
-                constexpr int opa = (c & 1) + 2 * h;
-                mfma_fp4<opb, opa>(acc[c][j], rb[r][j], ra[r][c], sbv[j / 2], sav[c / 2]);
-            });
-            __builtin_amdgcn_sched_barrier(0);
-        });
-    };
-
-    // ---- prologue --------------------------------------------------------
-    static_for<3>([&](auto P) {
-        constexpr int ps = decltype(P)::value;
-        constexpr int nd = T::DA + T::DB + (((ps & 1) == 0) ? T::DS : 0);
-        const uint32_t dead = dead_bits(ps);
-        static_for<nd>([&](auto D) { issue_item(P, D, ps, dead); });
-    });
-    wait_vmcnt<CNT_ODD + CNT_EVEN>();
-    barrier();
-    read_all(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
-
-    // ---- main loop: 4 stages per trip, ring slot = stage % 4 ----------
-    // The stage count is padded to a multiple of 4 with all-zero stages
-    // (zero data, zero scale bytes), which add exactly 0 to the sums.
-    const int n_st4 = (n_st + 3) & ~3;
-    for (int ls0 = 0; ls0 < n_st4; ls0 += 4) {
-        static_for<4>([&](auto U) { stage(U, ls0 + decltype(U)::value); });
-    }
-    // The look-ahead DMAs of the last trip are still writing LDS: drain them
-    // before this workgroup's LDS can be handed to another.
-    wait_vmcnt<0>();
-    mfma_drain();
-    static_for<T::FM>([&](auto i) {
-        static_for<T::FN>([&](auto j) { pin_after_drain(acc[i][j]); });
-    });
-
-    // ---- epilogue ----------------------------------------------------------
-    // Factors default to 1.0f, and x * (1.0f * 1.0f) == x exactly, so the
-    // no-factor case runs the same branch-free code.
-    const bool has_f = (p.Af != nullptr) && (p.Bf != nullptr);
-    const int row_l = wm * T::WM + (lane & 15);        // row within tile (frag 0)
-    const int col_w = n0 + wn * T::WN;                  // first column of the wave
-    const int colq = (lane >> 4) * 4;                   // lane's 4 columns in a frag
-    if constexpr (SPLIT) {
-        const rsrc_t rW = make_rsrc(p.ws + ((size_t)split * p.M + m0) * p.N,
-                                    (uint32_t)(rows_a * p.N * 4));
-        static_for<T::FN>([&](auto j) {
-            const int c = col_w + j * 16;
-            if (c < p.N) {
-                static_for<T::FM>([&](auto i) {
-                    store16(rW, (uint32_t)(((row_l + i * 16) * p.N + c + colq) * 4), acc[i][j]);
-                });
-            }
-        });
-    } else {
-        const rsrc_t rAf = make_rsrc(p.Af + m0, has_f ? (uint32_t)rows_a : 0u);
-        const rsrc_t rBf = make_rsrc(p.Bf, has_f ? (uint32_t)p.N : 0u);
-        const rsrc_t rBias = make_rsrc(p.bias, p.bias ? (uint32_t)(p.N * 2) : 0u);
-        const rsrc_t rO = make_rsrc(p.out + (size_t)m0 * p.N, (uint32_t)(rows_a * p.N * 2));
-        float fa[T::FM];
-        static_for<T::FM>([&](auto i) {
-            fa[i] = (has_f ? factor_of(load1(rAf, row_l + i * 16)) : 1.0f) * p.alpha;
-        });
-        static_for<T::FN>([&](auto j) {
-            const int c = col_w + j * 16;
-            if (c < p.N) {
-                const uint32_t bytes = (uint32_t)load4(rBf, c + colq);
-                float fb[4], bz[4] = {0.f, 0.f, 0.f, 0.f};
-                for (int q = 0; q < 4; ++q) fb[q] = has_f ? factor_of(bytes >> (8 * q)) : 1.0f;
-                if (p.bias) {
-                    const i32x2 bw = load8(rBias, (uint32_t)((c + colq) * 2));
-                    bz[0] = bf16_lo((uint32_t)bw[0]); bz[1] = bf16_hi((uint32_t)bw[0]);
-                    bz[2] = bf16_lo((uint32_t)bw[1]); bz[3] = bf16_hi((uint32_t)bw[1]);
-                }
-                static_for<T::FM>([&](auto i) {
-                    f32x4 v = acc[i][j];
-                    for (int q = 0; q < 4; ++q) v[q] = v[q] * (fa[i] * fb[q]);
-                    if (p.bias)
-                        for (int q = 0; q < 4; ++q) v[q] = add_nc(v[q], bz[q]);
-                    store8(rO, (uint32_t)(((row_l + i * 16) * p.N + c + colq) * 2),
-                           pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-                });
-            }
-        });
-    }
-}
-
-// ======================================================================
-// B-direct tiled kernel
-// ======================================================================
-// Same workgroup tiling as gemm_tiled_kernel, but only A goes through LDS:
-// the preshuffled B is already in MFMA fragment order (one 1-KiB
+// A workgroup of WGM x WGN waves computes BM x BN tiles.  Only A goes through
+// LDS: the preshuffled B is already in MFMA fragment order (one 1-KiB
 // contiguous block per 16 rows x 128 K), so each wave loads its B fragments
 // with plain 16-byte buffer loads straight into VGPRs, three stages ahead,
 // into a 4-deep register ring.  This halves the LDS traffic of the stage
@@ -397,6 +167,11 @@ struct BdShape {
     static_assert(NW == 1 ? NBC == 1 : NW >= 1 + NBC, "one factor DMA per wave");
     static_assert(BM % 16 == 0, "pair halves of whole 8-row DMA groups");
     static_assert(3 * PSLOT + 2 * SBUF <= 150 * 1024, "LDS budget");
+    // Epilogue stores staged through LDS (whole rows per neighbouring lanes)
+    // for tiles of 96+ rows; the 64-row tiles, whose short epilogues run with
+    // 2-4 workgroups per CU, store straight from registers (the staged form
+    // measured 0.7-4% slower there).
+    static constexpr bool STAGE_EPI = BM >= 96;
 };
 
 // One work unit of the persistent schedule (a tile and a K-split of it);
@@ -464,6 +239,8 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     __shared__ __attribute__((aligned(1024))) uint8_t sc0[T::SBUF];
     __shared__ __attribute__((aligned(1024))) uint8_t sc1[T::SBUF];
     __shared__ float ftab[256];
+    // Epilogue staging, per wave: 16 rows x 128 bytes (STAGE_EPI shapes).
+    __shared__ __attribute__((aligned(16))) uint8_t estage[T::STAGE_EPI ? T::NW : 1][2048];
     __shared__ uint32_t ftail;   // A factor bytes of rows Mdw.. M-1 (at most 3)
     // Pair slots of the current 4-stage iteration: q0 (pair 0, stages 0-1),
     // q1 (pair 1, stages 2-3), q2 (pair 2, DMA'd by stages 0-1); pair 3 (DMA'd
@@ -478,6 +255,8 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         else return q2;
     };
 
+    PhaseClock ph;
+    ph.start();
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = w / T::WGN, wn = w % T::WGN;
@@ -487,6 +266,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     const int n_st4 = (p.sps + 3) & ~3;
     // Grouped: the first M-tile index of each expert (prefix sums), in LDS.
     __shared__ int gtile[GROUPED ? kMaxGroups + 1 : 1];
+    __shared__ int gscan[GROUPED ? T::NT : 1];
     int tiles_m = p.tiles_m;
     // Expert e's rows, clamped into [0, M]: the offsets come from the device
     // and are not checked on the host, so no offset may move a store outside
@@ -495,20 +275,45 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     auto g_end = [&](int e) __attribute__((always_inline)) {
         return min(max(p.groups[e + 1], g_beg(e)), p.M);
     };
+    // M-tiles of expert e.  An expert whose first row is not a multiple of 32
+    // gets none (its rows are not written): the shuffled A scales come in
+    // 32-row groups, and a tile starting inside one would read the wrong
+    // scale bytes.  mbs_gemm_a4w4_check_groups reports such offsets.
+    auto g_tiles = [&](int e) __attribute__((always_inline)) {
+        const int b = g_beg(e);
+        return (b & 31) ? 0 : (g_end(e) - b + T::BM - 1) / T::BM;
+    };
     if constexpr (GROUPED) {
-        if (threadIdx.x == 0) {
-            int acc_t = 0;
-            for (int e = 0; e < p.n_groups; ++e) {
-                gtile[e] = acc_t;
-                acc_t += (g_end(e) - g_beg(e) + T::BM - 1) / T::BM;
-            }
-            gtile[p.n_groups] = acc_t;
-        }
+        // Prefix sums over the whole workgroup: thread t sums the experts of
+        // its contiguous chunk, the chunk sums are scanned in LDS
+        // (Hillis-Steele), and each thread writes its chunk's prefixes.
+        const int E = p.n_groups;
+        const int per = (E + T::NT - 1) / T::NT;
+        const int e0 = min((int)threadIdx.x * per, E), e1 = min(e0 + per, E);
+        int sum = 0;
+        for (int e = e0; e < e1; ++e) sum += g_tiles(e);
+        gscan[threadIdx.x] = sum;
         __syncthreads();
-        tiles_m = gtile[p.n_groups];
+        for (int d = 1; d < T::NT; d <<= 1) {
+            const int v = (int)threadIdx.x >= d ? gscan[threadIdx.x - d] : 0;
+            __syncthreads();
+            gscan[threadIdx.x] += v;
+            __syncthreads();
+        }
+        int run = gscan[threadIdx.x] - sum;
+        for (int e = e0; e < e1; ++e) {
+            gtile[e] = run;
+            run += g_tiles(e);
+        }
+        if (threadIdx.x == T::NT - 1) gtile[E] = gscan[T::NT - 1];
+        __syncthreads();
+        tiles_m = gtile[E];
     }
     const int tiles = tiles_m * p.tiles_n;
     const int units = tiles * p.splits;
+    // A grouped launch whose experts are all empty (or skipped) has no work;
+    // every workgroup leaves before its first load.
+    if (units == 0) return;
     const int G = gridDim.x;
     // Workgroups are dispatched round-robin over the 8 XCDs (private L2s).
     // With G % 8 == 0 the ids of one XCD are those with id % 8 == x; map
@@ -801,18 +606,26 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         // Everything issued two or more stages ago has landed (A of ls+1 for
         // this stage's look-ahead reads, B and scales of ls); the previous
         // stage's issues may still be in flight.
+        ph.mark((u == 0 && post) ? kPhNext : kPhBody);
+        ph.stage();
         if constexpr (u == 0) {
             if (!post) {
                 wait_vmcnt<NIP>();
+                ph.mark(kPhWait);
                 barrier();
+                ph.mark(kPhBar);
             }
         } else if constexpr (u == 1) {
             if (post) wait_vmcnt<NIP + EPI_OPS>();
             else wait_vmcnt<NIP>();
+            ph.mark(kPhWait);
             barrier();
+            ph.mark(kPhBar);
         } else {
             wait_vmcnt<NIP>();
+            ph.mark(kPhWait);
             barrier();
+            ph.mark(kPhBar);
         }
         __builtin_amdgcn_sched_barrier(0);
         Tgt t3;
@@ -1032,6 +845,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         q1 = q0;
         q0 = t;
     };
+    ph.mark(kPhPro);
     for (int id = blockIdx.x; id < units; id += G) {
         {   // first iteration, peeled: its stage 0 starts the accumulators
             const bool post = id != (int)blockIdx.x;
@@ -1055,8 +869,12 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         }
         // The next unit's first stage would wait and sync here; doing it now
         // also makes this unit's factor bytes (and the table) visible.
+        ph.mark(kPhBody);
+        ph.unit();
         wait_vmcnt<NI_ODD>();
+        ph.mark(kPhWait);
         barrier();
+        ph.mark(kPhBar);
         mfma_drain();
         static_for<T::FM>([&](auto i) {
             static_for<T::FN>([&](auto j) { pin_after_drain(acc[i][j]); });
@@ -1101,60 +919,151 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                         fa[i] = ftab[b] * p.alpha;
                     });
                 }
-                // Fragment pair (2p, 2p+1) covers 32 columns.  Lane (m, q) holds
-                // columns 4q..4q+3 of each; after the swaps it holds 8 consecutive
-                // columns 8q..8q+7 of the pair: a 16-byte store.  Stores are
-                // issued unconditionally (EPI_OPS): an out-of-range pair or half
-                // stores at kOOB, which the hardware drops.
-                static_for<T::FN / 2>([&](auto P2) {
-                    constexpr int j0 = 2 * decltype(P2)::value;
-                    const int c = col_w + j0 * 16;
+                // Fragment pair (j, j+1) covers 32 columns.  Lane (m, q) holds
+                // columns 4q..4q+3 of each; after two rounds of lane swaps it
+                // holds 8 consecutive columns 8q..8q+7 of the pair (16 bytes)
+                // of row m.  PairEpi: the pair's factor and bias operands.
+                struct PairEpi {
                     float f0[4], f1[4], z0[4], z1[4];
-                    const int cl = wn * T::WN + j0 * 16 + q * 4;   // lane's first column in the tile
+                };
+                auto pair_setup = [&](auto J0) __attribute__((always_inline)) {
+                    constexpr int j0 = decltype(J0)::value;
+                    PairEpi e;
                     if constexpr (hf) {
+                        const int cl = wn * T::WN + j0 * 16 + q * 4;   // lane's first column in the tile
                         const uint32_t b0 = *reinterpret_cast<const uint32_t*>(&fbytes[par][256 + cl]);
                         const uint32_t b1 = *reinterpret_cast<const uint32_t*>(&fbytes[par][256 + cl + 16]);
                         static_for<4>([&](auto K4) {
                             constexpr int k = decltype(K4)::value;
-                            f0[k] = ftab[(b0 >> (8 * k)) & 255];
-                            f1[k] = ftab[(b1 >> (8 * k)) & 255];
+                            e.f0[k] = ftab[(b0 >> (8 * k)) & 255];
+                            e.f1[k] = ftab[(b1 >> (8 * k)) & 255];
                         });
                         const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&fbias[par][cl]);
                         const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&fbias[par][cl + 16]);
                         const uint32_t u0 = w0[0], u1 = w0[1], u2 = w1[0], u3 = w1[1];
-                        z0[0] = bf16_lo(u0); z0[1] = bf16_hi(u0); z0[2] = bf16_lo(u1); z0[3] = bf16_hi(u1);
-                        z1[0] = bf16_lo(u2); z1[1] = bf16_hi(u2); z1[2] = bf16_lo(u3); z1[3] = bf16_hi(u3);
+                        e.z0[0] = bf16_lo(u0); e.z0[1] = bf16_hi(u0); e.z0[2] = bf16_lo(u1); e.z0[3] = bf16_hi(u1);
+                        e.z1[0] = bf16_lo(u2); e.z1[1] = bf16_hi(u2); e.z1[2] = bf16_lo(u3); e.z1[3] = bf16_hi(u3);
                     }
-                    // N % 16 == 0: the pair is all in, only its first half, or out
-                    const bool store_ok = c < p.N && (c + 16 < p.N || q < 2);
-                    static_for<T::FM>([&](auto i) {
-                        f32x4 v0 = acc[i][j0], v1 = acc[i][j0 + 1];
-                        if constexpr (hf) {
-                            static_for<4>([&](auto K4) {
-                                constexpr int k = decltype(K4)::value;
-                                v0[k] = add_nc(v0[k] * (fa[i] * f0[k]), z0[k]);
-                                v1[k] = add_nc(v1[k] * (fa[i] * f1[k]), z1[k]);
-                            });
-                        }
-                        uint32_t x0 = pack_bf16x2(v0[0], v0[1]), x1 = pack_bf16x2(v0[2], v0[3]);
-                        uint32_t y0 = pack_bf16x2(v1[0], v1[1]), y1 = pack_bf16x2(v1[2], v1[3]);
-                        // round A: upper half of x <-> lower half of y
-                        auto a0 = __builtin_amdgcn_permlane32_swap(x0, y0, false, false);
-                        auto a1 = __builtin_amdgcn_permlane32_swap(x1, y1, false, false);
-                        // round B: odd rows of x <-> even rows of y
-                        auto b0s = __builtin_amdgcn_permlane16_swap(a0[0], a0[1], false, false);
-                        auto b1s = __builtin_amdgcn_permlane16_swap(a1[0], a1[1], false, false);
-                        const uint32_t o = (uint32_t)(((row_l + i * 16) * p.N + c + q * 8) * 2);
-                        i32x4 v = {(int)b0s[0], (int)b1s[0], (int)b0s[1], (int)b1s[1]};
-                        store16(rO, store_ok ? o : kOOB, __builtin_bit_cast(f32x4, v));
+                    return e;
+                };
+                // bf16 bits of pair (j0, j0+1) of row fragment i, lane (m, q):
+                // row m, columns 8q..8q+7 of the pair.
+                auto pair_bits = [&](auto I, auto J0, const PairEpi& e, uint32_t (&o)[4])
+                    __attribute__((always_inline)) {
+                    constexpr int i = decltype(I)::value, j0 = decltype(J0)::value;
+                    f32x4 v0 = acc[i][j0], v1 = acc[i][j0 + 1];
+                    if constexpr (hf) {
+                        static_for<4>([&](auto K4) {
+                            constexpr int k = decltype(K4)::value;
+                            v0[k] = add_nc(v0[k] * (fa[i] * e.f0[k]), e.z0[k]);
+                            v1[k] = add_nc(v1[k] * (fa[i] * e.f1[k]), e.z1[k]);
+                        });
+                    }
+                    uint32_t x0 = pack_bf16x2(v0[0], v0[1]), x1 = pack_bf16x2(v0[2], v0[3]);
+                    uint32_t y0 = pack_bf16x2(v1[0], v1[1]), y1 = pack_bf16x2(v1[2], v1[3]);
+                    // round A: upper half of x <-> lower half of y
+                    auto a0 = __builtin_amdgcn_permlane32_swap(x0, y0, false, false);
+                    auto a1 = __builtin_amdgcn_permlane32_swap(x1, y1, false, false);
+                    // round B: odd rows of x <-> even rows of y
+                    auto b0s = __builtin_amdgcn_permlane16_swap(a0[0], a0[1], false, false);
+                    auto b1s = __builtin_amdgcn_permlane16_swap(a1[0], a1[1], false, false);
+                    o[0] = b0s[0]; o[1] = b1s[0]; o[2] = b0s[1]; o[3] = b1s[1];
+                };
+                auto vec_of = [](const uint32_t (&o)[4]) __attribute__((always_inline)) {
+                    i32x4 v = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+                    return __builtin_bit_cast(f32x4, v);
+                };
+                // Stores go through a per-wave LDS staging area so that
+                // consecutive lanes write consecutive 16-byte chunks of one
+                // row.  In the swapped-operand MFMA layout lane (m, q) holds row
+                // m, so a direct store has neighbouring lanes in 16 different
+                // rows; staged, 8 neighbouring lanes cover one 128-byte line.
+                // Measured (graph replays, same bytes): 0.95-0.99x the time of
+                // the direct 16-row x 64-byte stores on 256x256 tiles, epilogue
+                // 8.6K -> 6.8K cycles per tile at 8192^3.  Chunks are
+                // XOR-swizzled by row (conflict-free writes and reads).  Stores
+                // are issued unconditionally (EPI_OPS): a lane past N stores at
+                // kOOB, which the hardware drops.  A wave's LDS accesses run in
+                // order, so its next block may overwrite the area right after
+                // the reads; the compiler's lgkmcnt wait before each store
+                // covers the reads.
+                uint8_t* const stg = estage[T::STAGE_EPI ? w : 0];
+                if constexpr (!T::STAGE_EPI) {
+                    // straight from registers: 16 rows x 64 bytes per store
+                    static_for<T::FN / 2>([&](auto P2) {
+                        constexpr int j0 = 2 * decltype(P2)::value;
+                        const PairEpi e = pair_setup(std::integral_constant<int, j0>{});
+                        const int c = col_w + j0 * 16;
+                        // N % 16 == 0: the pair is all in, only its first half, or out
+                        const bool store_ok = c < p.N && (c + 16 < p.N || q < 2);
+                        static_for<T::FM>([&](auto I) {
+                            constexpr int i = decltype(I)::value;
+                            uint32_t u[4];
+                            pair_bits(I, std::integral_constant<int, j0>{}, e, u);
+                            const uint32_t o = (uint32_t)(((row_l + i * 16) * p.N + c + q * 8) * 2);
+                            store16(rO, store_ok ? o : kOOB, vec_of(u));
+                            __builtin_amdgcn_sched_barrier(0);
+                        });
+                    });
+                    return;
+                }
+                // Fragment quads (j0..j0+3, 64 columns = one 128-byte line of a
+                // row): lane (m, q) writes row m, chunks q (pair j0) and 4+q
+                // (pair j0+2) of a 16 x 128-byte block; lane L reads back row
+                // L/8 (+8 for the second store), chunk L%8.
+                constexpr int NQ = T::FN / 4;
+                static_for<NQ>([&](auto Q4) {
+                    constexpr int j0 = 4 * decltype(Q4)::value;
+                    const PairEpi e0 = pair_setup(std::integral_constant<int, j0>{});
+                    const PairEpi e1 = pair_setup(std::integral_constant<int, j0 + 2>{});
+                    const int m = lane & 15, r = lane >> 3, cc = lane & 7;
+                    uint8_t* const w0 = stg + m * 128 + ((q ^ (m & 7)) * 16);
+                    uint8_t* const w1 = stg + m * 128 + (((4 + q) ^ (m & 7)) * 16);
+                    const uint8_t* const r0 = stg + r * 128 + ((cc ^ r) * 16);
+                    const int col = col_w + j0 * 16 + cc * 8;   // N % 16 == 0
+                    const bool store_ok = col < p.N;
+                    static_for<T::FM>([&](auto I) {
+                        constexpr int i = decltype(I)::value;
+                        uint32_t u[4], v[4];
+                        pair_bits(I, std::integral_constant<int, j0>{}, e0, u);
+                        pair_bits(I, std::integral_constant<int, j0 + 2>{}, e1, v);
+                        *reinterpret_cast<f32x4*>(w0) = vec_of(u);
+                        *reinterpret_cast<f32x4*>(w1) = vec_of(v);
+                        const f32x4 x0 = *reinterpret_cast<const f32x4*>(r0);
+                        const f32x4 x1 = *reinterpret_cast<const f32x4*>(r0 + 1024);
+                        const uint32_t o = (uint32_t)(((wm * T::WM + i * 16 + r) * p.N + col) * 2);
+                        store16(rO, store_ok ? o : kOOB, x0);
+                        store16(rO, store_ok ? o + (uint32_t)(8 * p.N * 2) : kOOB, x1);
                         // keep the accumulator reads of later blocks from being
                         // hoisted here (register pressure)
                         __builtin_amdgcn_sched_barrier(0);
                     });
                 });
+                // A trailing pair (FN % 4 == 2): a 16 x 64-byte block, lane L
+                // reads back row L/4, chunk L%4 (4 neighbouring lanes per row).
+                if constexpr (T::FN % 4 == 2) {
+                    constexpr int j0 = T::FN - 2;
+                    const PairEpi e = pair_setup(std::integral_constant<int, j0>{});
+                    const int m = lane & 15, r = lane >> 2, cc = lane & 3;
+                    uint8_t* const w0 = stg + m * 64 + ((q ^ ((m >> 1) & 3)) * 16);
+                    const uint8_t* const r0 = stg + r * 64 + ((cc ^ ((r >> 1) & 3)) * 16);
+                    const int col = col_w + j0 * 16 + cc * 8;
+                    const bool store_ok = col < p.N;
+                    static_for<T::FM>([&](auto I) {
+                        constexpr int i = decltype(I)::value;
+                        uint32_t u[4];
+                        pair_bits(I, std::integral_constant<int, j0>{}, e, u);
+                        *reinterpret_cast<f32x4*>(w0) = vec_of(u);
+                        const f32x4 x0 = *reinterpret_cast<const f32x4*>(r0);
+                        const uint32_t o = (uint32_t)(((wm * T::WM + i * 16 + r) * p.N + col) * 2);
+                        store16(rO, store_ok ? o : kOOB, x0);
+                        __builtin_amdgcn_sched_barrier(0);
+                    });
+                }
             };
             epi(std::integral_constant<bool, AFF>{});
         }
+        ph.mark(kPhEpi);
         par ^= 1;
         factor_dma(nxt, par);
         bias_dma(nxt, par);
@@ -1165,7 +1074,10 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     }
     // The last unit prefetched dead stages into LDS and registers: let every
     // transfer land before the workgroup's LDS is released.
+    ph.mark(kPhEpi);
     wait_vmcnt<0>();
+    ph.mark(kPhEpi);
+    ph.flush(p.phase);
 }
 
 // ======================================================================
@@ -1305,19 +1217,6 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
 }
 
 template <class T>
-hipError_t launch_tiled(const GemmArgs& a, dim3 grid, bool ktail, bool split, hipStream_t s)
-{
-    if (ktail) {
-        if (split) hipLaunchKernelGGL((gemm_tiled_kernel<T, true, true>), grid, dim3(T::NT), 0, s, a);
-        else hipLaunchKernelGGL((gemm_tiled_kernel<T, true, false>), grid, dim3(T::NT), 0, s, a);
-    } else {
-        if (split) hipLaunchKernelGGL((gemm_tiled_kernel<T, false, true>), grid, dim3(T::NT), 0, s, a);
-        else hipLaunchKernelGGL((gemm_tiled_kernel<T, false, false>), grid, dim3(T::NT), 0, s, a);
-    }
-    return hipGetLastError();
-}
-
-template <class T>
 hipError_t launch_bdirect(const GemmArgs& a, dim3 grid, bool gen, bool split, hipStream_t s)
 {
     const bool aff = affine_epilogue(a);
@@ -1356,14 +1255,6 @@ hipError_t launch_skinny(const GemmArgs& a, dim3 grid, bool, bool split, hipStre
     return hipGetLastError();
 }
 
-using T256x256 = TileShape<256, 256, 2, 2>;
-using T256x128 = TileShape<256, 128, 2, 2>;
-using T128x256 = TileShape<128, 256, 2, 2>;
-using T128x128 = TileShape<128, 128, 2, 2>;
-using T64x256 = TileShape<64, 256, 1, 4>;
-using T64x128 = TileShape<64, 128, 1, 2>;
-using T64x64 = TileShape<64, 64, 1, 1>;
-
 using B256x256 = BdShape<256, 256, 2, 2>;
 using B256x128 = BdShape<256, 128, 2, 2>;
 using B128x256 = BdShape<128, 256, 2, 2>;
@@ -1381,7 +1272,6 @@ using B128x256w14 = BdShape<128, 256, 1, 4>;
 
 
 // Launcher instantiations, one translation unit per group (gemm_inst_*.hip).
-#define MBS_TILED_SHAPES(X) X(T256x256) X(T256x128) X(T128x256) X(T128x128) X(T64x256) X(T64x128) X(T64x64)
 #define MBS_BDIRECT_SHAPES_A(X) X(B256x256) X(B256x128) X(B128x256) X(B128x128)
 #define MBS_BDIRECT_SHAPES_B(X) X(B64x256) X(B64x128) X(B64x64) X(B256x128w14)
 #define MBS_BDIRECT_SHAPES_C(X) X(B256x256w14) X(B192x256w14) X(B96x256w14)
@@ -1390,12 +1280,10 @@ using B128x256w14 = BdShape<128, 256, 1, 4>;
 #define MBS_SKINNY_SHAPES(X) X(1, 2, 16, 4) X(2, 2, 16, 4) X(1, 2, 8, 4) X(2, 2, 8, 4) X(1, 1, 8, 8) X(2, 1, 8, 8) X(2, 2, 4, 4)
 
 #define MBS_LAUNCH_SIG const GemmArgs&, dim3, bool, bool, hipStream_t
-#define MBS_TILED_INST(T) template hipError_t launch_tiled<T>(MBS_LAUNCH_SIG);
 #define MBS_BDIRECT_INST(T) template hipError_t launch_bdirect<T>(MBS_LAUNCH_SIG);
 #define MBS_SKINNY_INST(a, b, c, d) template hipError_t launch_skinny<a, b, c, d>(MBS_LAUNCH_SIG);
 #define MBS_GROUPED_INST(T) template hipError_t launch_bdirect_grouped<T>(MBS_LAUNCH_SIG);
 #define MBS_GROUPED_EXTERN(T) extern template hipError_t launch_bdirect_grouped<T>(MBS_LAUNCH_SIG);
-#define MBS_TILED_EXTERN(T) extern template hipError_t launch_tiled<T>(MBS_LAUNCH_SIG);
 #define MBS_BDIRECT_EXTERN(T) extern template hipError_t launch_bdirect<T>(MBS_LAUNCH_SIG);
 #define MBS_SKINNY_EXTERN(a, b, c, d) extern template hipError_t launch_skinny<a, b, c, d>(MBS_LAUNCH_SIG);
 

@@ -309,6 +309,9 @@ int fmt_fail(const char* m)
     return MBS_ERR_ARGUMENT;
 }
 int scale_pad_of(int K) { return ((K + 31) / 32 + 7) / 8 * 8; }
+// The kernels read and write bf16 rows, packed bytes and fp32 output in
+// 16-byte (packed codes of the quantizers: 4-byte) units.
+bool misaligned(const void* p, uintptr_t a) { return p && reinterpret_cast<uintptr_t>(p) % a != 0; }
 unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 int launched()
 {
@@ -333,6 +336,8 @@ int mbs_quantize_mxfp4_bf16(const void* x, int rows, int K, uint8_t* packed,
 {
     if (!x || !packed) return fmt_fail("null pointer");
     if (rows < 1 || K < 32 || K % 32) return fmt_fail("need rows >= 1 and K % 32 == 0");
+    if (misaligned(x, 16) || misaligned(packed, 4))
+        return fmt_fail("x must be 16-byte and packed 4-byte aligned");
     if (K / 512 >= 65535) return fmt_fail("K too large for the quantizer grid");
     if (pad_byte < 0 || pad_byte > 255) return fmt_fail("pad_byte must be a byte");
     (void)hipGetLastError();
@@ -353,6 +358,8 @@ int mbs_quantize_mxfp4_mbs_bf16(const void* x, int rows, int K, uint8_t* packed,
 {
     if (!x || !packed || !factors) return fmt_fail("null pointer");
     if (rows < 1 || K < 32 || K % 32) return fmt_fail("need rows >= 1 and K % 32 == 0");
+    if (misaligned(x, 16) || misaligned(packed, 4))
+        return fmt_fail("x must be 16-byte and packed 4-byte aligned");
     if (pad_byte < 0 || pad_byte > 255) return fmt_fail("pad_byte must be a byte");
     (void)hipGetLastError();
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -374,6 +381,7 @@ int mbs_shuffle_b(const uint8_t* w, uint8_t* out, int N, int K, void* stream)
     if (!w || !out) return fmt_fail("null pointer");
     if (N < 16 || N % 16 || K < 64 || K % 64) return fmt_fail("need N % 16 == 0 and K % 64 == 0");
     if (w == out) return fmt_fail("shuffle_b is out of place");
+    if (misaligned(w, 16) || misaligned(out, 16)) return fmt_fail("w and out must be 16-byte aligned");
     (void)hipGetLastError();
     hipLaunchKernelGGL(shuffle_b_kernel, dim3(blocks_for((int64_t)N * (K / 32))), dim3(256), 0,
                        static_cast<hipStream_t>(stream), w, out, N, K / 2);
@@ -400,6 +408,7 @@ int mbs_unshuffle_b(const uint8_t* in, uint8_t* w, int N, int K, void* stream)
     if (!in || !w) return fmt_fail("null pointer");
     if (N < 16 || N % 16 || K < 64 || K % 64) return fmt_fail("need N % 16 == 0 and K % 64 == 0");
     if (in == w) return fmt_fail("unshuffle_b is out of place");
+    if (misaligned(in, 16) || misaligned(w, 16)) return fmt_fail("in and w must be 16-byte aligned");
     (void)hipGetLastError();
     hipLaunchKernelGGL(unshuffle_b_kernel, dim3(blocks_for((int64_t)N * (K / 32))), dim3(256), 0,
                        static_cast<hipStream_t>(stream), in, w, N, K / 2);
@@ -437,6 +446,8 @@ int mbs_dequant_mxfp4(const uint8_t* packed, const uint8_t* scale_shuffled, floa
     if (rows < 1 || K < 32 || K % 32) return fmt_fail("need rows >= 1 and K % 32 == 0");
     if (b_preshuffled && (rows % 16 || K % 64))
         return fmt_fail("preshuffled layout needs rows % 16 == 0 and K % 64 == 0");
+    if (misaligned(packed, 16) || misaligned(out, 16))
+        return fmt_fail("packed and out must be 16-byte aligned");
     (void)hipGetLastError();
     hipLaunchKernelGGL(dequant_kernel, dim3(blocks_for((int64_t)rows * (K / 32))), dim3(256), 0,
                        static_cast<hipStream_t>(stream), packed, scale_shuffled, out, rows, K,

@@ -261,8 +261,8 @@ def epilogue_bf16(c, a_factor=None, b_factor=None) -> np.ndarray:
 def epilogue_affine_bf16(c, a_factor=None, b_factor=None, alpha: float = 1.0,
                         bias_bits=None) -> np.ndarray:
     """The affine epilogue (no reference counterpart in its own launcher; the
-    aiter assembly kernel it benchmarks against has alpha and bias,
-    asm_vs_wg_kernel.md:85-87): in fp32, c * ((f(a)[m] * alpha) * f(b)[n]),
+    aiter GEMM its harness calls next to it takes a bias,
+    test_gemm_a4w4.py:95-123): in fp32, c * ((f(a)[m] * alpha) * f(b)[n]),
     plus bias[n] (bf16 bits) when given, then bf16 RNE (uint16 bits).  The
     factors are 1 when absent.  With alpha 1 and no bias this is
     epilogue_bf16."""

@@ -95,6 +95,45 @@ def test_launch_rejects_null_and_half_factors():
     assert b"together" in L.mbs_last_error()
 
 
+@pytest.mark.parametrize("which,off,why", [
+    ("A", 8, "16-byte"), ("B", 4, "16-byte"), ("As", 1, "16-byte"), ("Bs", 8, "16-byte"),
+    ("out", 2, "16-byte"), ("Af", 2, "4-byte"), ("Bf", 1, "4-byte"),
+])
+def test_launch_rejects_misaligned_operands(which, off, why):
+    """Every kernel moves A, B, the scales and the output in 16-byte units and
+    the factor bytes in dwords: a misaligned base is refused before any GPU call."""
+    L = c_lib()
+    ptrs = dict(A=FAKE, B=FAKE, As=FAKE, Bs=FAKE, Af=FAKE, Bf=FAKE, out=FAKE)
+    ptrs[which] += off
+    st = L.mbs_gemm_a4w4_launch(ptrs["A"], ptrs["B"], ptrs["As"], ptrs["Bs"], ptrs["Af"], ptrs["Bf"],
+                                ptrs["out"], 128, 256, 512, 128, 16, None, 0, None)
+    assert st == 1
+    assert why in L.mbs_last_error().decode()
+
+
+def test_format_entry_points_reject_misaligned():
+    L = c_lib()
+    P, I = ctypes.c_void_p, ctypes.c_int
+    L.mbs_shuffle_b.argtypes = [P, P, I, I, P]
+    L.mbs_quantize_mxfp4_bf16.argtypes = [P, I, I, P, P, P, I, P]
+    L.mbs_dequant_mxfp4.argtypes = [P, P, P, I, I, I, P]
+    assert L.mbs_shuffle_b(FAKE + 4, FAKE + 4096, 32, 512, None) == 1
+    assert L.mbs_quantize_mxfp4_bf16(FAKE + 2, 4, 64, FAKE, None, None, 127, None) == 1
+    assert L.mbs_quantize_mxfp4_bf16(FAKE, 4, 64, FAKE + 1, None, None, 127, None) == 1
+    assert L.mbs_dequant_mxfp4(FAKE, FAKE, FAKE + 8, 16, 64, 1, None) == 1
+    assert b"aligned" in L.mbs_last_error()
+
+
+def test_check_groups_validates_arguments():
+    L = c_lib()
+    P, I = ctypes.c_void_p, ctypes.c_int
+    L.mbs_gemm_a4w4_check_groups.argtypes = [P, I, I, P, P]
+    assert L.mbs_gemm_a4w4_check_groups(None, 2, 64, FAKE, None) == 1
+    assert L.mbs_gemm_a4w4_check_groups(FAKE, 0, 64, FAKE, None) == 1
+    assert L.mbs_gemm_a4w4_check_groups(FAKE, 2, -1, FAKE, None) == 1
+    assert L.mbs_gemm_a4w4_check_groups(FAKE + 2, 2, 64, FAKE, None) == 1
+
+
 def test_plans_cover_every_config_shape():
     from mbs_amd import synthetic
 
@@ -107,7 +146,7 @@ def test_plans_cover_every_config_shape():
             if M <= 32:
                 assert name.startswith("skinny"), (M, N, K, name)
             else:
-                assert name.split("_")[0] in ("tiled", "bdirect"), (M, N, K, name)
+                assert name.startswith("bdirect"), (M, N, K, name)
     L.mbs_gemm_a4w4_plan_name(8192, 8192, 8192, buf, 256)
     assert "_256x256_" in buf.value.decode()
     assert L.mbs_gemm_a4w4_workspace_bytes(8192, 8192, 8192) == 0
@@ -142,5 +181,5 @@ def test_torch_module_rejects_host_tensors_and_bad_shapes():
     with pytest.raises(RuntimeError):
         m.quantize_mxfp4(torch.zeros(4, 64, dtype=torch.bfloat16))
     assert m.num_configs() >= 8
-    assert m.config_name(0).startswith("tiled")
+    assert all(m.config_name(c).startswith(("bdirect", "skinny")) for c in range(m.num_configs()))
     assert "skinny" in m.plan_name(1, 8192, 8192)

@@ -250,3 +250,37 @@ def test_output_past_2gib(dev):
         assert_close(got, ref, f"config {cfg} splits {splits}")
         del out
         torch.cuda.empty_cache()
+
+
+def test_misaligned_views(dev, gold):
+    """Operands that are views starting off a 16-byte boundary (factors off a
+    4-byte one): the module copies them into aligned storage and gives the
+    aligned call's bytes; the C ABI refuses them (MBS_ERR_ARGUMENT)."""
+    import torch
+
+    import mbs_amd
+    from gpu_util import clib, ptr, stream_ptr
+
+    c = Case(gold["x_packed"], gold["x_scales"], gold["w_packed"], gold["w_scales"],
+             gold["a_factor"], gold["b_factor"])
+    say("misaligned operand views")
+    want = mbs_amd.gemm_a4w4(c.A, c.B, c.As, c.Bs, c.Af, c.Bf)
+
+    def shifted(t, off):
+        buf = torch.empty(t.numel() + off, dtype=torch.uint8, device=t.device)
+        v = buf[off:].view(t.shape)
+        v.copy_(t)
+        return v
+
+    for off in (1, 4, 8):
+        views = [shifted(t, off) for t in (c.A, c.B, c.As, c.Bs, c.Af, c.Bf)]
+        assert views[0].data_ptr() % 16 != 0
+        got = mbs_amd.gemm_a4w4(*views)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), off
+    L = clib()
+    out = torch.empty(c.Mpad, c.N, dtype=torch.bfloat16, device=c.A.device)
+    A8 = shifted(c.A, 8)
+    st = L.mbs_gemm_a4w4_launch(ptr(A8), ptr(c.B), ptr(c.As), ptr(c.Bs), None, None, ptr(out), c.M,
+                                c.N, c.K, c.Mpad, c.snp, None, 0, stream_ptr())
+    assert st == 1 and b"aligned" in L.mbs_last_error()

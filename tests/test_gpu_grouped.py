@@ -163,3 +163,93 @@ def test_grouped_rejects_bad_offsets(dev):
     for bad in ([0, 48, 128], [0, 96, 64], [32, 64, 128], [0, 64, 160]):
         with pytest.raises(RuntimeError, match="group_offsets"):
             mbs_amd.gemm_a4w4_grouped(A, B, As, Bs, torch.tensor(bad, dtype=torch.int32))
+
+
+def _grouped_c_call(dev, A, B, As, Bs, goff, E, M, N, K, out, config=-1):
+    """mbs_gemm_a4w4_grouped_launch through the C ABI into a caller-filled output."""
+    import ctypes
+
+    import mbs_amd
+    from gpu_util import ptr, stream_ptr
+
+    L = mbs_amd.clib()
+    P, I = ctypes.c_void_p, ctypes.c_int
+    L.mbs_gemm_a4w4_grouped_launch.argtypes = [P, P, P, P, P, P, P, I, P, I, I, I, I, I, I, P]
+    L.mbs_gemm_a4w4_grouped_launch.restype = I
+    snp = oracle.scale_pad(K)
+    return L.mbs_gemm_a4w4_grouped_launch(ptr(A), ptr(B), ptr(As), ptr(Bs), None, None, ptr(goff),
+                                          E, ptr(out), M, N, K, oracle.round_up(M, 32), snp, config,
+                                          stream_ptr())
+
+
+@pytest.mark.parametrize("config", [0, 1, 2, 3])
+def test_grouped_all_experts_empty_writes_nothing(dev, config):
+    """Every expert empty (offsets all 0) with M > 0: the kernel has no work
+    units; every workgroup leaves before its first load and the output keeps
+    the caller's bytes."""
+    import torch
+
+    say(f"grouped all-empty config={config}")
+    rng = np.random.default_rng(5)
+    M, N, K = 64, 256, 512
+    _, xp, xs, wq, _, _, _ = make_problem(rng, [64, 0], N, K)
+    A, As, B, Bs, _, _ = device_operands(dev, M, N, K, xp, xs, wq, None, None)
+    out = torch.full((M, N), 7.0, dtype=torch.bfloat16, device=dev)
+    goff = torch.zeros(3, dtype=torch.int32, device=dev)
+    assert _grouped_c_call(dev, A, B, As, Bs, goff, 2, M, N, K, out, config) == 0
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())
+
+
+def test_grouped_unaligned_expert_is_skipped_and_reported(dev):
+    """An expert whose first row is not a multiple of 32 gets no tiles (its
+    rows keep the caller's bytes); the aligned experts are still exact, and
+    check_groups / validate=True report the offsets."""
+    import torch
+
+    import mbs_amd
+
+    say("grouped unaligned expert start")
+    rng = np.random.default_rng(9)
+    N, K = 256, 512
+    M, xp, xs, wq, _, _, _ = make_problem(rng, [64, 32, 64], N, K)
+    offs = np.array([0, 64, 80, 160], np.int32)    # expert 2 starts at row 80
+    A, As, B, Bs, _, _ = device_operands(dev, M, N, K, xp, xs, wq, None, None)
+    goff = torch.from_numpy(offs).to(dev)
+    assert mbs_amd.check_groups(goff, M) == (1, 0)
+    assert mbs_amd.check_groups(torch.tensor([0, 64, 32, 200], dtype=torch.int32, device=dev), M) == (0, 2)
+    with pytest.raises(RuntimeError, match="not a multiple of 32"):
+        mbs_amd.gemm_a4w4_grouped(A, B, As, Bs, goff, validate=True)
+    out = torch.full((M, N), 3.0, dtype=torch.bfloat16, device=dev)
+    assert _grouped_c_call(dev, A, B, As, Bs, goff, 3, M, N, K, out) == 0
+    torch.cuda.synchronize()
+    assert bool((out[80:160] == 3.0).all())
+    for e, (r0, r1) in enumerate([(0, 64), (64, 80)]):
+        ref = oracle.bf16_bits_to_f32(oracle.run_torch(xp[r0:r1], wq[e][0], xs[r0:r1], wq[e][1]))
+        assert_close(bf16_to_f32(out[r0:r1]), ref, f"expert {e}")
+    assert mbs_amd.check_groups(torch.from_numpy(np.array([0, 64, 96, 160], np.int32)).to(dev), M) == (0, 0)
+
+
+def test_grouped_many_experts(dev):
+    """256 experts (most empty, the prefix sums span every thread of the
+    workgroup scan): bit-identical to the dense launch per non-empty expert."""
+    import torch
+
+    import mbs_amd
+
+    E, N, K = 256, 128, 512
+    rows = [0] * E
+    for e in (0, 1, 63, 64, 130, 200, 254, 255):
+        rows[e] = 32 * (1 + e % 3)
+    say(f"grouped E={E} N={N} K={K}")
+    rng = np.random.default_rng(11)
+    M, xp, xs, wq, af, bf, offs = make_problem(rng, rows, N, K)
+    A, As, B, Bs, _, _ = device_operands(dev, M, N, K, xp, xs, wq, None, None)
+    for config in range(mbs_amd.ext().grouped_num_configs()):
+        got = mbs_amd.gemm_a4w4_grouped(A, B, As, Bs, torch.from_numpy(offs).to(dev), config=config,
+                                        validate=True)
+        torch.cuda.synchronize()
+        for e in range(E):
+            if rows[e]:
+                want = dense_expert(dev, e, offs, N, K, xp, xs, wq, None, None)
+                assert torch.equal(got[offs[e]:offs[e + 1]], want), (config, e)
