@@ -72,6 +72,132 @@ def time_steps(fn, steps, warmup):
     return e0.elapsed_time(e1) / 1e3, wall   # seconds (events), seconds (host clock)
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def graph_blocks(fn, launches=100, blocks=7):
+    """The reference's timing method (asm_vs_wg_kernel.md:179-180): a HIP
+    graph of `launches` back-to-back calls (L2 warm), replayed `blocks` times;
+    returns the per-launch microseconds of every block."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(launches):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    out = []
+    for _ in range(blocks):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        out.append(e0.elapsed_time(e1) * 1e3 / launches)
+    del g
+    return out
+
+
+def phase_lib():
+    """ctypes handle on the phase-timer build of the C library, or None."""
+    import ctypes
+
+    import mbs_amd
+
+    path = os.path.join(mbs_amd.LIB_DIR, "libmbs_gemm_phase.so")
+    if not os.path.exists(path):
+        return None
+    L = ctypes.CDLL(path)
+    P, I, S = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    L.mbs_gemm_a4w4_launch.argtypes = [P, P, P, P, P, P, P, I, I, I, I, I, P, S, P]
+    L.mbs_gemm_a4w4_launch.restype = I
+    L.mbs_gemm_a4w4_workspace_bytes.argtypes = [I, I, I]
+    L.mbs_gemm_a4w4_workspace_bytes.restype = S
+    L.mbs_phase_timer_attach.argtypes = [P]
+    L.mbs_phase_timer_slots.restype = I
+    return L
+
+
+PHASES = ("prologue", "stage_wait", "barrier", "stage_body", "epilogue", "next_unit")
+
+
+def phase_split(ops, M, N, K, launches=20):
+    """In-kernel cycle split of the persistent GEMM on operands `ops` (the
+    phase-timer build: s_memtime per phase per wave), with the shader clock
+    from s_memtime / s_memrealtime and the kernel time with and without the
+    timer (HIP events, eager launches)."""
+    import ctypes
+
+    import torch
+
+    import mbs_amd
+
+    L = phase_lib()
+    if L is None:
+        return {"error": "libmbs_gemm_phase.so not built (python -m mbs_amd._build --phase-timer)"}
+    A, B, As, Bs = ops
+    dev = A.device
+    Mpad, snp = mbs_amd.round_up(M, 32), mbs_amd.scale_pad(K)
+    out = torch.empty(Mpad, N, dtype=torch.bfloat16, device=dev)
+    wsb = L.mbs_gemm_a4w4_workspace_bytes(M, N, K)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    slots = L.mbs_phase_timer_slots()
+    sums = torch.zeros(1024 * slots, dtype=torch.int64, device=dev)   # per workgroup
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    strm = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def call():
+        st = L.mbs_gemm_a4w4_launch(p(A), p(B), p(As), p(Bs), None, None, p(out), M, N, K, Mpad, snp,
+                                    p(ws), wsb, strm())
+        assert st == 0, st
+
+    def timed(n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / n
+
+    L.mbs_phase_timer_attach(None)
+    for _ in range(5):
+        call()
+    torch.cuda.synchronize()
+    us_plain = timed(launches)
+    L.mbs_phase_timer_attach(p(sums))
+    us_timed = timed(launches)
+    L.mbs_phase_timer_attach(None)
+    v = [int(x) for x in sums.view(1024, slots).sum(0).cpu().tolist()]
+    cyc = dict(zip(PHASES, v[:len(PHASES)]))
+    total = sum(cyc.values())
+    stages, units, clk, rt = v[len(PHASES):len(PHASES) + 4]
+    res = {
+        "shape": [M, N, K], "plan": mbs_amd.ext().plan_name(M, N, K), "launches": launches,
+        "kernel_us_plain": round(us_plain, 2), "kernel_us_timed": round(us_timed, 2),
+        "sclk_mhz": round(clk / rt * 100.0, 1) if rt else None,
+        "wave_cycles": total,
+        "fraction": {k: round(c / total, 4) for k, c in cyc.items()} if total else None,
+        "cycles_per_stage": {k: round(cyc[k] / stages, 1) for k in ("stage_wait", "barrier", "stage_body")}
+        if stages else None,
+        "epilogue_cycles_per_unit": round(cyc["epilogue"] / units, 1) if units else None,
+        "next_unit_cycles_per_unit": round(cyc["next_unit"] / units, 1) if units else None,
+        "stages": stages, "units": units,
+    }
+    return res
+
+
 def decode_bench(dev, Ms=(1, 4, 16, 32), N=8192, K=8192, copies=10, replays=20):
     """Cold (rotating copies) and warm per-launch time of the decode shapes,
     from HIP-graph replay so host launch overhead is excluded.  Also, cold,
@@ -222,7 +348,9 @@ def grouped_bench(dev, experts=8, rows=256, shapes=((7168, 2048), (4096, 7168), 
 
 def cpu_baseline(x, w, rows=8192, reps=3):
     """The oracle's run_torch restatement (dequant to fp32, torch.mm fp32,
-    bf16) on this host: `rows` rows of the config-1 A against the full W."""
+    bf16) on this host: `rows` rows of the config-1 A against the full W.
+    The three steps are timed separately (median of `reps` each) and the
+    total is their sum: run_torch runs them one after the other."""
     import torch
 
     import oracle  # the CPU checker; timed here as the reported baseline
@@ -232,18 +360,65 @@ def cpu_baseline(x, w, rows=8192, reps=3):
     xp, xs = oracle.quantize_mxfp4(x[:rows].float().numpy())
     wp, ws = oracle.quantize_mxfp4(w.float().numpy())
     N, K = w.shape
-    times = []
+    t_dq, t_mm, t_bf = [], [], []
     for _ in range(reps):
         t0 = time.perf_counter()
-        oracle.run_torch(xp, wp, xs, ws)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
+        xf = oracle.dequant_mxfp4(xp, xs)
+        wf = oracle.dequant_mxfp4(wp, ws)
+        t1 = time.perf_counter()
+        c = torch.mm(torch.from_numpy(xf), torch.from_numpy(wf).T).numpy()
+        t2 = time.perf_counter()
+        oracle.epilogue_bf16(c)
+        t3 = time.perf_counter()
+        t_dq.append(t1 - t0)
+        t_mm.append(t2 - t1)
+        t_bf.append(t3 - t2)
+        del xf, wf, c
+    dq, mm, bf = (statistics.median(t) for t in (t_dq, t_mm, t_bf))
+    t = dq + mm + bf
+    flops = 2.0 * rows * N * K
     return {
-        "value": round(2.0 * rows * N * K / t / 1e12, 4), "unit": "TFLOPS", "cores": cores,
-        "kind": "port",
-        "sample": f"config-1 rows 0..{rows - 1} of A x full W ({rows}x{N}x{K}): dequant + fp32 "
-                  f"torch.mm + bf16, median of {reps} ({t:.2f} s each)",
+        "value": round(flops / t / 1e12, 4), "unit": "TFLOPS", "cores": cores, "kind": "port",
+        "cpu_model": cpu_model(),
+        "dequant_s": round(dq, 3), "matmul_s": round(mm, 3), "bf16_s": round(bf, 3),
+        "total_s": round(t, 3), "matmul_TFLOPS": round(flops / mm / 1e12, 4),
+        "sample": f"config-1 rows 0..{rows - 1} of A x full W ({rows}x{N}x{K}): oracle dequant (C) "
+                  f"+ fp32 torch.mm + bf16, each step median of {reps}",
     }
+
+
+def shape_bench(M, N, K, iters):
+    """One shape, as the reference's bench_one.py drives it (bench_one.py:1-48):
+    bf16 x, w ~ N(0,1) quantized to MXFP4, 10 warmup calls, then `iters`
+    timed calls of gemm_a4w4 between two events on the current stream."""
+    import torch
+
+    import mbs_amd
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    w = torch.randn(N, K, generator=g, device=dev).to(torch.bfloat16)
+    A, As = mbs_amd.quantize_mxfp4(x, shuffle=True)
+    Wp, Bs = mbs_amd.quantize_mxfp4(w, shuffle=True)
+    B = mbs_amd.shuffle_weight(Wp)
+    call = lambda: mbs_amd.gemm_a4w4(A, B, As, Bs)
+    for _ in range(10):
+        call()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / iters
+    tflops = M * N * K * 2 / us / 1e6
+    print(f"mbs  M={M} N={N} K={K}  {us:8.2f} us  {tflops:8.1f} TFLOPS", flush=True)
+    print(json.dumps({"shape": [M, N, K], "us": round(us, 3), "TFLOPS": round(tflops, 1),
+                      "TB/s_ref": round((A.numel() + B.numel()) / us / 1e6, 4),
+                      "plan": mbs_amd.ext().plan_name(M, N, K), "iters": iters}), flush=True)
 
 
 def main():
@@ -258,6 +433,13 @@ def main():
     ap.add_argument("--decode-only", action="store_true",
                     help="only run the decode shapes (cold and warm graph replays) and print "
                          "their block; for counter runs of the decode kernel")
+    ap.add_argument("--shape", type=str, default=None, metavar="M,N,K",
+                    help="only time one shape the way the reference's bench_one.py does "
+                         "(10 warmup + --iters timed calls) and print it")
+    ap.add_argument("--iters", type=int, default=50, help="timed calls of --shape")
+    ap.add_argument("--phase-split", action="store_true",
+                    help="only print the in-kernel phase split of configs[1] (or --shape) from "
+                         "the phase-timer build")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 20 device-to-device copies of MIB MiB (scales the HBM "
                          "FETCH_SIZE/WRITE_SIZE counters) and exit")
@@ -286,6 +468,15 @@ def main():
     if args.decode_only:
         print(json.dumps({"decode": decode_bench(dev)}), flush=True)
         return
+    if args.shape and not args.phase_split:
+        M, N, K = (int(v) for v in args.shape.split(","))
+        shape_bench(M, N, K, args.iters)
+        return
+    if args.phase_split:
+        M, N, K = (int(v) for v in args.shape.split(",")) if args.shape else (8192, 8192, 8192)
+        ops, _ = prepare(M, N, K, 1, dev)
+        print(json.dumps({"phase_split": phase_split(ops, M, N, K)}), flush=True)
+        return
     M = N = K = 8192
     (A, B, As, Bs), (x, w) = prepare(M, N, K, 1, dev)
     step = lambda: mbs_amd.gemm_a4w4(A, B, As, Bs)
@@ -295,6 +486,12 @@ def main():
     tflops = flops * args.steps / t_step / 1e12
     kern_us = t_ev / args.steps * 1e6
     achieved = flops / (kern_us * 1e-6) / 1e12
+    # the reference's method: median of 7 graph-replayed blocks of 100 launches
+    blocks = graph_blocks(step)
+    med = statistics.median(blocks)
+    # the shader clock the kernel runs at, from the phase-timer build
+    # (s_memtime / s_memrealtime inside the same kernel on the same operands)
+    ph = phase_split((A, B, As, Bs), M, N, K, launches=10)
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_cfg1.json")
@@ -313,6 +510,17 @@ def main():
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP4_TFLOPS, 4),
                      "traffic": traffic, "kernel_us": round(kern_us, 2),
                      "algorithmic_bytes": algo_bytes(M, N, K)},
+        "graph_replay": {"method": "7 blocks x 100 launches, HIP graph, L2 warm (the reference's)",
+                         "us_median": round(med, 2), "us_blocks": [round(b, 2) for b in blocks],
+                         "TFLOPS_median": round(flops / med / 1e6, 1),
+                         "frac_median": round(flops / med / 1e6 / PEAK_FP4_TFLOPS, 4)},
+        # the reference's narrow "TB/s" column: packed A and B only
+        # (test_gemm_a4w4.py:168-170)
+        "TBps_ref": round((A.numel() + B.numel()) / kern_us / 1e6, 4),
+        "sclk_mhz": ph.get("sclk_mhz"),
+        "sclk_source": "s_memtime / s_memrealtime inside the GEMM kernel (phase-timer build, "
+                       "same operands, 10 launches after the timed block)",
+        "peak_at_sclk": round(PEAK_FP4_TFLOPS * ph["sclk_mhz"] / 2400.0, 1) if ph.get("sclk_mhz") else None,
     }
     if not args.no_decode:
         line["decode"] = decode_bench(dev)
