@@ -87,6 +87,29 @@ int mbs_gemm_a4w4_launch_ex(int config, int splits, const uint8_t* A, const uint
                             int scaleN_pad, float alpha, const void* bias, void* workspace,
                             size_t workspace_bytes, void* stream);
 
+/* Bytes of device scratch the allocation-free entry point owns per GPU. */
+#define MBS_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* mbs_gemm_a4w4_launch_ex without a workspace argument, for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  It
+ * calls no hipMalloc/hipFree: split-K partials go to a static device array of
+ * MBS_NOALLOC_SCRATCH_BYTES per GPU (looked up with hipGetSymbolAddress on the
+ * first call on each device that needs it, with that device current; the
+ * stream must belong to the current device).  config < 0: the heuristic plan,
+ * limited to plans whose partials fit the scratch; config >= 0 with splits <= 0:
+ * that config's split choice, or no split when it does not fit; an explicit
+ * split count whose partials exceed the scratch returns MBS_ERR_WORKSPACE.
+ * Nothing in the scratch needs to start at zero (every split writes its whole
+ * partial plane before the reduce reads it).  All calls on one GPU share its
+ * scratch: calls whose launches overlap on that GPU (different streams, no
+ * ordering between them) race and must not be made. */
+int mbs_gemm_a4w4_launch_noalloc(int config, int splits, const uint8_t* A, const uint8_t* B,
+                                 const uint8_t* AScale, const uint8_t* BScale,
+                                 const uint8_t* AFactor, const uint8_t* BFactor, void* out, int M,
+                                 int N, int K, int Mpad, int scaleN_pad, float alpha,
+                                 const void* bias, void* stream);
+
 /* Grouped (mixture-of-experts) GEMM: E = num_groups experts share one launch.
  * Expert e owns rows [group_offsets[e], group_offsets[e+1]) of A (and of out)
  * and the e-th block of the stacked weights:

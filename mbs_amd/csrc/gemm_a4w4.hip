@@ -25,9 +25,17 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 namespace mbs {
+
+// Scratch of the allocation-free entry point (mbs_gemm_a4w4_launch_noalloc):
+// its split-K partials live here instead of in a caller workspace.  Each GPU
+// the library runs on holds its own copy until the process ends.  In host
+// code `scratch` is only a symbol handle; its address on a device comes from
+// hipGetSymbolAddress with that device current (scratch_on_current_device).
+static __device__ __align__(256) uint8_t scratch[MBS_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 thread_local std::string g_last_error;
@@ -530,6 +538,32 @@ int run_grouped(int g, const uint8_t* A, const uint8_t* B, const uint8_t* As, co
     return MBS_OK;
 }
 
+// Device address of `scratch` on the current device, looked up once per
+// device (nullptr if the lookup fails; the error text is recorded).
+constexpr int kMaxDevices = 64;
+void* scratch_on_current_device()
+{
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_last_error("no current HIP device for the scratch buffer");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            set_last_error((std::string("hipGetSymbolAddress(scratch) failed: ") +
+                            hipGetErrorString(e)).c_str());
+            return nullptr;
+        }
+        addr[dev] = ptr;
+    }
+    return addr[dev];
+}
+
 }  // namespace
 }  // namespace mbs
 
@@ -716,5 +750,47 @@ int mbs_gemm_a4w4_launch_ex(int config, int splits, const uint8_t* A, const uint
 void mbs_phase_timer_attach(unsigned long long* sums) { g_phase = sums; }
 int mbs_phase_timer_slots(void) { return kPhSlots; }
 #endif
+
+int mbs_gemm_a4w4_launch_noalloc(int config, int splits, const uint8_t* A, const uint8_t* B,
+                                 const uint8_t* AScale, const uint8_t* BScale,
+                                 const uint8_t* AFactor, const uint8_t* BFactor, void* out, int M,
+                                 int N, int K, int Mpad, int scaleN_pad, float alpha,
+                                 const void* bias, void* stream)
+{
+    set_last_error("");
+    int st = validate(A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, Mpad, scaleN_pad);
+    if (st != MBS_OK) return st;
+    if (!(alpha == alpha)) return fail(MBS_ERR_ARGUMENT, "alpha is NaN");
+    if (config >= kNumConfigs)
+        return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) + " out of range");
+    if (M == 0) return MBS_OK;
+    const size_t cap = MBS_NOALLOC_SCRATCH_BYTES;
+    Plan pl;
+    if (config < 0) {
+        // the heuristic, limited to plans whose partials fit the scratch
+        if (!choose_plan(M, N, K, cap, &pl))
+            return fail(MBS_ERR_CONFIG, "no kernel configuration fits this problem");
+    } else {
+        if (!make_plan(config, splits, M, N, K, &pl))
+            return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) + " cannot run M=" +
+                                            std::to_string(M));
+        // the config's own split choice falls back to no split when its
+        // partials do not fit; an explicit split count is refused
+        if (pl.ws_bytes > cap && splits <= 0 && !make_plan(config, 1, M, N, K, &pl))
+            return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) + " cannot run M=" +
+                                            std::to_string(M));
+    }
+    if (pl.ws_bytes > cap)
+        return fail(MBS_ERR_WORKSPACE, "split-K partials need " + std::to_string(pl.ws_bytes) +
+                                           " bytes; the allocation-free entry point has " +
+                                           std::to_string(cap) + " bytes of scratch");
+    void* ws = nullptr;
+    if (pl.ws_bytes) {
+        ws = scratch_on_current_device();
+        if (!ws) return MBS_ERR_LAUNCH;
+    }
+    return run_plan(pl, A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, scaleN_pad, ws,
+                    pl.ws_bytes, stream, alpha, bias);
+}
 
 }  // extern "C"
