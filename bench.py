@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MXFP4 A4W4 GEMM on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 150]
 
 Headline workload: C[8192,8192] bf16 =
 dequant(A)·dequant(B)^T with M=N=K=8192, operands drawn by the seeded
@@ -196,6 +196,57 @@ def phase_split(ops, M, N, K, launches=20):
         "stages": stages, "units": units,
     }
     return res
+
+
+def stream_floor(dev, nbytes=None, copies=10, replays=20, grids=(256, 512, 1024, 2048)):
+    """The streaming-read floor of the decode shapes: libmbs_probe.so reads
+    `nbytes` (default: the bytes of a decode GEMM at N=K=8192, M=1) with
+    16-byte non-temporal loads, cold over `copies` rotating buffers (more
+    than the 256 MB MALL), graph-replayed; best grid of `grids`."""
+    import ctypes
+
+    import torch
+
+    import mbs_amd
+
+    path = os.path.join(mbs_amd.LIB_DIR, "libmbs_probe.so")
+    if not os.path.exists(path):
+        return {"error": "libmbs_probe.so not built"}
+    L = ctypes.CDLL(path)
+    L.mbs_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
+                                        ctypes.c_void_p]
+    if nbytes is None:
+        nbytes = (algo_bytes(1, 8192, 8192) + 4095) // 4096 * 4096
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1) for _ in range(copies)]
+    sink = torch.empty(max(grids) * 4, dtype=torch.int32, device=dev)
+    res = {}
+    for grid in grids:
+        def run():
+            st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for b in bufs:
+                assert L.mbs_probe_stream_read(ctypes.c_void_p(b.data_ptr()), nbytes,
+                                               ctypes.c_void_p(sink.data_ptr()), grid, st) == 0
+        run()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            run()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        res[grid] = e0.elapsed_time(e1) * 1e3 / (replays * copies)
+        del g
+    best = min(res, key=res.get)
+    us = res[best]
+    return {"bytes": nbytes, "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1),
+            "frac_hbm": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), "grid": best,
+            "us_by_grid": {str(k): round(v, 3) for k, v in res.items()},
+            "method": f"cold, {copies} rotating buffers, graph of {copies} launches replayed {replays}x"}
 
 
 def decode_bench(dev, Ms=(1, 4, 16, 32), N=8192, K=8192, copies=10, replays=20):
@@ -424,8 +475,12 @@ def shape_bench(M, N, K, iters):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # Defaults: under sustained fp4 MFMA load the GPU's power management
+    # first lowers the clock (launches ~10-25 after idle run up to 35% slower)
+    # and settles after ~100 launches (profiles/gemm_cfg1_power_ramp.txt); 150
+    # warmup launches put the 200 timed ones in the settled state (~80 ms).
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=150)
     ap.add_argument("--no-decode", action="store_true", help="skip the decode shapes")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-grouped", action="store_true", help="skip the grouped (MoE) shapes")
@@ -440,6 +495,12 @@ def main():
     ap.add_argument("--phase-split", action="store_true",
                     help="only print the in-kernel phase split of configs[1] (or --shape) from "
                          "the phase-timer build")
+    ap.add_argument("--sustain", type=int, default=0, metavar="N",
+                    help="only run N back-to-back eager launches of configs[1] after 1 s idle and "
+                         "print their event times (for a kernel trace of the clock's response)")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the graph-replayed blocks and the in-kernel clock measurement "
+                         "(hardware-counter runs see only the timed launches)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 20 device-to-device copies of MIB MiB (scales the HBM "
                          "FETCH_SIZE/WRITE_SIZE counters) and exit")
@@ -466,7 +527,24 @@ def main():
 
     dev = torch.device("cuda:0")
     if args.decode_only:
-        print(json.dumps({"decode": decode_bench(dev)}), flush=True)
+        print(json.dumps({"decode": decode_bench(dev), "stream_floor": stream_floor(dev)}), flush=True)
+        return
+    if args.sustain:
+        ops, _ = prepare(8192, 8192, 8192, 1, dev)
+        step = lambda: mbs_amd.gemm_a4w4(*ops)
+        step()
+        torch.cuda.synchronize()
+        time.sleep(1.0)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.sustain)]
+        for e0, e1 in ev:
+            e0.record()
+            step()
+            e1.record()
+        torch.cuda.synchronize()
+        us = [round(e0.elapsed_time(e1) * 1e3, 1) for e0, e1 in ev]
+        print(json.dumps({"sustain_us": us, "first8_mean": round(statistics.mean(us[:8]), 1),
+                          "last50_mean": round(statistics.mean(us[-50:]), 1)}), flush=True)
         return
     if args.shape and not args.phase_split:
         M, N, K = (int(v) for v in args.shape.split(","))
@@ -487,11 +565,11 @@ def main():
     kern_us = t_ev / args.steps * 1e6
     achieved = flops / (kern_us * 1e-6) / 1e12
     # the reference's method: median of 7 graph-replayed blocks of 100 launches
-    blocks = graph_blocks(step)
+    blocks = [0.0] if args.no_extras else graph_blocks(step)
     med = statistics.median(blocks)
     # the shader clock the kernel runs at, from the phase-timer build
     # (s_memtime / s_memrealtime inside the same kernel on the same operands)
-    ph = phase_split((A, B, As, Bs), M, N, K, launches=10)
+    ph = {} if args.no_extras else phase_split((A, B, As, Bs), M, N, K, launches=10)
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_cfg1.json")
@@ -512,8 +590,8 @@ def main():
                      "algorithmic_bytes": algo_bytes(M, N, K)},
         "graph_replay": {"method": "7 blocks x 100 launches, HIP graph, L2 warm (the reference's)",
                          "us_median": round(med, 2), "us_blocks": [round(b, 2) for b in blocks],
-                         "TFLOPS_median": round(flops / med / 1e6, 1),
-                         "frac_median": round(flops / med / 1e6 / PEAK_FP4_TFLOPS, 4)},
+                         "TFLOPS_median": round(flops / med / 1e6, 1) if med else None,
+                         "frac_median": round(flops / med / 1e6 / PEAK_FP4_TFLOPS, 4) if med else None},
         # the reference's narrow "TB/s" column: packed A and B only
         # (test_gemm_a4w4.py:168-170)
         "TBps_ref": round((A.numel() + B.numel()) / kern_us / 1e6, 4),
@@ -524,6 +602,7 @@ def main():
     }
     if not args.no_decode:
         line["decode"] = decode_bench(dev)
+        line["decode"]["stream_floor"] = stream_floor(dev)
     del A, B, As, Bs
     if not args.no_grouped:
         line["grouped"] = grouped_bench(dev)

@@ -5,6 +5,8 @@ Products (under ``mbs_amd/lib/``):
 * ``libmbs_gemm_kernel.so`` -- the torch-free HIP library with the C ABI of
   ``include/mbs_gemm_a4w4.h`` (GEMM + format kernels), built with hipcc for
   gfx950 only.
+* ``libmbs_probe.so`` -- a measurement tool: the streaming-read floor of a
+  decode GEMM (``include/mbs_probe.h``).
 * ``mbs_gemm_a4w4<EXT_SUFFIX>.so`` -- the torch/pybind11 module that is the
   drop-in for the reference's ``mbs_gemm_a4w4`` extension; host-only C++
   (built with g++), linked against the library above with an ``$ORIGIN``
@@ -50,6 +52,9 @@ HIP_FLAGS = [
 ]
 
 KERNEL_LIB = os.path.join(LIB, "libmbs_gemm_kernel.so")
+# Measurement tool beside the GEMM library: the streaming-read floor of a
+# decode GEMM (include/mbs_probe.h; bench.py loads it).
+PROBE_LIB = os.path.join(LIB, "libmbs_probe.so")
 # The same kernels with the in-kernel phase timer compiled in (a measurement
 # tool: bench.py --phase-split and the sclk figure of the bench line).
 PHASE_LIB = os.path.join(LIB, "libmbs_gemm_phase.so")
@@ -83,6 +88,13 @@ def build_kernel_lib(phase_timer: bool = False) -> str:
     _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp])
     os.replace(tmp, out)
     return out
+
+
+def build_probe_lib() -> str:
+    os.makedirs(LIB, exist_ok=True)
+    _run([HIPCC, *HIP_FLAGS, "-shared", os.path.join(CSRC, "stream_probe.hip"), "-o", PROBE_LIB + ".tmp"])
+    os.replace(PROBE_LIB + ".tmp", PROBE_LIB)
+    return PROBE_LIB
 
 
 def build_module() -> str:
@@ -124,6 +136,7 @@ def build_oracle() -> None:
 def build_all(with_oracle: bool = True) -> None:
     build_kernel_lib()
     build_module()
+    build_probe_lib()
     if with_oracle:
         build_oracle()
 

@@ -1089,13 +1089,15 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
 // (from L2: A is shared by every workgroup) feeds NF MFMAs.  B is read
 // once, with the non-temporal policy; up to U stages of B, A and scales
 // are in flight per wave.  Waves reduce their partial tiles through LDS
-// in a fixed order (deterministic), then NF*MT waves run the epilogue.
+// in a fixed order (deterministic), then the waves run the epilogue of the
+// NF*MT output fragments.  NF = 1 covers half a 32-row scale group; NF =
+// 2*G covers G whole groups (one B-scale dword per group and 256 K).
 template <int MT, int NF, int NWK, int U, bool SPLIT>
 __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
 {
     static_assert(U % 2 == 0, "batch must cover whole 256-K scale groups");
-    static_assert(NF == 1 || NF == 2, "one 32-row scale group per workgroup");
-    static_assert(NF * MT <= NWK, "one epilogue wave per output fragment");
+    static_assert(NF == 1 || NF % 2 == 0, "whole 32-row scale groups (or half of one)");
+    constexpr int NG = (NF + 1) / 2;   // 32-row B-scale groups per workgroup
     __shared__ f32x4 red[NWK][NF * MT][64];
 
     const int lane = threadIdx.x & 63;
@@ -1118,7 +1120,9 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
     const rsrc_t rB = make_rsrc(p.B + (size_t)(n0 >> 4) * fstride, (uint32_t)nfrag * fstride);
     const rsrc_t rA = make_rsrc(p.A, (uint32_t)(p.M * Kp));
     const rsrc_t rAs = make_rsrc(p.As, (uint32_t)(32 * p.snp));
-    const rsrc_t rBs = make_rsrc(p.Bs + (size_t)(n0 >> 5) * 32 * p.snp, (uint32_t)(32 * p.snp));
+    const int Npad = (p.N + 31) & ~31;
+    const rsrc_t rBs = make_rsrc(p.Bs + (size_t)(n0 >> 5) * 32 * p.snp,
+                                 (uint32_t)(min(NG * 32, Npad - ((n0 >> 5) << 5)) * p.snp));
     const bool hi_lane = lane >= 32;
     const bool ktail = (K & 127) != 0;
     // NF == 1: the workgroup's 16 rows are the low or high half of a 32-row
@@ -1132,14 +1136,16 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
 
     for (int st = my_begin; st < my_end; st += U) {
         i32x4 b[U][NF], a[U][MT];
-        int sb[U / 2], sa[U / 2];
+        int sb[U / 2][NG], sa[U / 2];
         // Scales first: loads return in issue order, so stage u's MFMAs then
         // wait only for stage u's B and A, and the MFMAs trail the stream
         // instead of starting after the whole batch has landed.
         static_for<U / 2>([&](auto v) {
             const int g = (st >> 1) + v;
             const bool ok = st + 2 * v < my_end;
-            sb[v] = load4(rBs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
+            static_for<NG>([&](auto G) {
+                sb[v][G] = load4(rBs, ok ? (uint32_t)(G * 32 * p.snp + g * 256 + lane * 4) : kOOB);
+            });
             sa[v] = load4(rAs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
         });
         static_for<U>([&](auto u) {
@@ -1162,14 +1168,14 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
         static_for<U>([&](auto u) {
             constexpr int h = u & 1;
             const int s = st + u;
-            int sbv = sb[u / 2] >> sshift;
-            int sav = sa[u / 2];
             const bool tail = ktail && s == S_total - 1 && hi_lane;
-            sbv = tail ? 0x7F7F7F7F : sbv;
+            int sav = sa[u / 2];
             sav = tail ? 0x7F7F7F7F : sav;
             static_for<NF>([&](auto f) {
+                int sbv = sb[u / 2][f / 2] >> sshift;
+                sbv = tail ? 0x7F7F7F7F : sbv;
                 static_for<MT>([&](auto m) {
-                    mfma_fp4<f + 2 * h, m + 2 * h>(acc[f][m], b[u][f], a[u][m], sbv, sav);
+                    mfma_fp4<(f & 1) + 2 * h, m + 2 * h>(acc[f][m], b[u][f], a[u][m], sbv, sav);
                 });
             });
         });
@@ -1183,36 +1189,37 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
         static_for<MT>([&](auto m) { red[kw][f * MT + m][lane] = acc[f][m]; });
     });
     __syncthreads();
-    if (kw >= NF * MT) return;
-    const int f = kw / MT, m = kw % MT;
-    if (n0 + 16 * f >= p.N) return;
-
-    f32x4 v = red[0][kw][lane];
-    for (int k = 1; k < NWK; ++k) v += red[k][kw][lane];
-    const int c = n0 + 16 * f + (lane >> 4) * 4;
-    const int row = 16 * m + (lane & 15);
-    if constexpr (SPLIT) {
-        const rsrc_t rW = make_rsrc(p.ws + (size_t)split * p.M * p.N, (uint32_t)(p.M * p.N * 4));
-        store16(rW, (uint32_t)((row * p.N + c) * 4), v);
-    } else {
-        if (p.Af && p.Bf) {
-            const rsrc_t rAf = make_rsrc(p.Af, (uint32_t)p.M);
-            const rsrc_t rBf = make_rsrc(p.Bf, (uint32_t)p.N);
-            const float fa = factor_of(load1(rAf, row)) * p.alpha;
-            const uint32_t bytes = (uint32_t)load4(rBf, c);
-            for (int q = 0; q < 4; ++q) v[q] = v[q] * (fa * factor_of(bytes >> (8 * q)));
-        } else if (p.alpha != 1.0f) {
-            for (int q = 0; q < 4; ++q) v[q] = v[q] * p.alpha;
+    // output fragment o = f * MT + m, handled by wave o % NWK
+    for (int o = kw; o < NF * MT; o += NWK) {
+        const int f = o / MT, m = o % MT;
+        if (n0 + 16 * f >= p.N) continue;
+        f32x4 v = red[0][o][lane];
+        for (int k = 1; k < NWK; ++k) v += red[k][o][lane];
+        const int c = n0 + 16 * f + (lane >> 4) * 4;
+        const int row = 16 * m + (lane & 15);
+        if constexpr (SPLIT) {
+            const rsrc_t rW = make_rsrc(p.ws + (size_t)split * p.M * p.N, (uint32_t)(p.M * p.N * 4));
+            store16(rW, (uint32_t)((row * p.N + c) * 4), v);
+        } else {
+            if (p.Af && p.Bf) {
+                const rsrc_t rAf = make_rsrc(p.Af, (uint32_t)p.M);
+                const rsrc_t rBf = make_rsrc(p.Bf, (uint32_t)p.N);
+                const float fa = factor_of(load1(rAf, row)) * p.alpha;
+                const uint32_t bytes = (uint32_t)load4(rBf, c);
+                for (int q = 0; q < 4; ++q) v[q] = v[q] * (fa * factor_of(bytes >> (8 * q)));
+            } else if (p.alpha != 1.0f) {
+                for (int q = 0; q < 4; ++q) v[q] = v[q] * p.alpha;
+            }
+            if (p.bias) {
+                const rsrc_t rBias = make_rsrc(p.bias, (uint32_t)(p.N * 2));
+                const i32x2 bw = load8(rBias, (uint32_t)(c * 2));
+                v[0] = add_nc(v[0], bf16_lo((uint32_t)bw[0])); v[1] = add_nc(v[1], bf16_hi((uint32_t)bw[0]));
+                v[2] = add_nc(v[2], bf16_lo((uint32_t)bw[1])); v[3] = add_nc(v[3], bf16_hi((uint32_t)bw[1]));
+            }
+            const rsrc_t rO = make_rsrc(p.out, (uint32_t)(p.M * p.N * 2));
+            store8(rO, (uint32_t)((row * p.N + c) * 2), pack_bf16x2(v[0], v[1]),
+                   pack_bf16x2(v[2], v[3]));
         }
-        if (p.bias) {
-            const rsrc_t rBias = make_rsrc(p.bias, (uint32_t)(p.N * 2));
-            const i32x2 bw = load8(rBias, (uint32_t)(c * 2));
-            v[0] = add_nc(v[0], bf16_lo((uint32_t)bw[0])); v[1] = add_nc(v[1], bf16_hi((uint32_t)bw[0]));
-            v[2] = add_nc(v[2], bf16_lo((uint32_t)bw[1])); v[3] = add_nc(v[3], bf16_hi((uint32_t)bw[1]));
-        }
-        const rsrc_t rO = make_rsrc(p.out, (uint32_t)(p.M * p.N * 2));
-        store8(rO, (uint32_t)((row * p.N + c) * 2), pack_bf16x2(v[0], v[1]),
-               pack_bf16x2(v[2], v[3]));
     }
 }
 
