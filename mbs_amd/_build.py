@@ -16,7 +16,8 @@ Run ``python -m mbs_amd._build`` (or ``__graft_entry__.build()``).  Every call
 rebuilds.  ``python -m mbs_amd._build --phase-timer`` builds
 ``libmbs_gemm_phase.so`` instead: the same kernels with the in-kernel phase
 timer (``MBS_PHASE_TIMER=1``, ``include/mbs_phase_timer.h``), a measurement
-tool.
+tool.  ``--incremental`` keeps object files newer than every source and
+header (development builds; ``build()`` always rebuilds everything).
 """
 from __future__ import annotations
 
@@ -68,10 +69,21 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"build step failed: {os.path.basename(cmd[0])} -> {cmd[-1]}")
 
 
+def _newest_input(src: str) -> float:
+    heads = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    heads += [os.path.join(INCLUDE, f) for f in os.listdir(INCLUDE) if f.endswith(".h")]
+    return max(os.path.getmtime(p) for p in [os.path.join(CSRC, src), *heads])
+
+
+INCREMENTAL = False   # --incremental: keep objects newer than every source and header
+
+
 def _hip_object(src: str, phase_timer: bool = False) -> str:
     sub = "_obj_phase" if phase_timer else "_obj"
     obj = os.path.join(LIB, sub, os.path.splitext(src)[0] + ".o")
     os.makedirs(os.path.dirname(obj), exist_ok=True)
+    if INCREMENTAL and os.path.exists(obj) and os.path.getmtime(obj) > _newest_input(src):
+        return obj
     extra = ["-DMBS_PHASE_TIMER=1"] if phase_timer else []
     _run([HIPCC, *HIP_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
     return obj
@@ -142,6 +154,7 @@ def build_all(with_oracle: bool = True) -> None:
 
 
 if __name__ == "__main__":
+    INCREMENTAL = "--incremental" in sys.argv[1:]
     if "--phase-timer" in sys.argv[1:]:
         print("built", build_kernel_lib(phase_timer=True))
     else:

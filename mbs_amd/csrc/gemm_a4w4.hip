@@ -290,9 +290,11 @@ double plan_cost(const Plan& pl, int M, int N, int K)
 // Measured best plans (graph-replayed timings of every configuration and
 // split count on MI355X) for the shapes of the reference's published model
 // layers, the BASELINE configurations and a few squares.  Exact matches
-// take these; every other shape goes through the cost model.  Three entries
-// were re-measured after the XCD tile groups became 4 rows tall (two sweeps,
-// with and without factors, same winner both times; both ranges quoted).
+// take these; every other shape goes through the cost model.  Entries with
+// "a / b us" were re-measured after the epilogue stores moved to LDS staging:
+// medians of 7 interleaved rounds of the candidates, without / with MBS
+// factors (a sweep run in order is biased by the clock's response to
+// sustained load).
 struct TunedPlan {
     int M, N, K;
     const char* config;
@@ -302,19 +304,19 @@ const TunedPlan kTuned[] = {
     {1024, 17408, 5120, "bdirect_128x384_w1x4", 1},  // 54.6-55.3 us (192x256: 56.6-57.9)
     {1024, 1024, 5120, "bdirect_64x128_w1x2", 1},  // 10.7 us
     {256, 7168, 2048, "bdirect_64x128_w1x2", 1},  // 7.1 us
-    {2048, 7168, 2048, "bdirect_256x256_w2x2", 1},  // 22.2 us
+    {2048, 7168, 2048, "bdirect_256x256_w1x4", 1},  // 20.2 / 22.3 us (256x256 2x2: 20.9 / 22.4)
     {256, 4096, 7168, "bdirect_64x128_w1x2", 1},  // 13.1 us
     {2048, 4096, 7168, "bdirect_128x256_w1x4", 1},  // 30.3 us
     {256, 2112, 7168, "bdirect_64x128_w1x2", 2},  // 13.1 us
-    {2048, 2112, 7168, "bdirect_256x128_w1x4", 1},  // 25.6-25.9 us (96x256: 27.0-27.3)
+    {2048, 2112, 7168, "bdirect_128x256_w1x4", 1},  // 23.9 / 24.5 us (256x128 1x4: 25.0 / 25.8)
     {1000, 1280, 512, "bdirect_64x128_w1x2", 1},  // 4.9 us
     {3333, 5120, 512, "bdirect_64x128_w1x2", 1},  // 15.3 us
-    {1000, 5120, 12288, "bdirect_256x128_w1x4", 1},  // 40.1 us
-    {3333, 1280, 12288, "bdirect_256x128_w1x4", 1},  // 38.3-38.6 us (128x256: 39.2-40.0)
+    {1000, 5120, 12288, "bdirect_128x256_w1x4", 1},  // 39.1 / 38.1 us (256x128 1x4: 41.7 / 40.0)
+    {3333, 1280, 12288, "bdirect_128x256_w1x4", 1},  // 38.1 / 38.6 us (256x128 1x4: 38.9 / 39.1; 96x256: 38.4 / 38.1)
     {8192, 10240, 5120, "bdirect_256x256_w2x2", 1},  // 186.5 us
     {8192, 17408, 5120, "bdirect_192x256_w1x4", 1},  // 327.5 us
     {8192, 5120, 17408, "bdirect_256x256_w2x2", 1},  // 295.7 us
-    {8192, 12288, 5120, "bdirect_128x384_w1x4", 1},  // 226.4 us
+    {8192, 12288, 5120, "bdirect_256x256_w1x4", 1},  // 238.0 / 235.8 us (128x384: 258.7 / 249.6)
     {8192, 8192, 8192, "bdirect_256x256_w2x2", 1},  // 219.7 us
     {128, 256, 512, "bdirect_64x64_w1x1", 1},  // 4.5 us
     {4096, 4096, 4096, "bdirect_256x256_w2x2", 1},  // 35.3 us
@@ -482,10 +484,10 @@ struct TunedGrouped {
     const char* dense;
 };
 const TunedGrouped kTunedGrouped[] = {
-    // two sweeps each: us of the chosen / the cost model's pick (64x256 or 64x128)
-    {2048, 7168, 2048, 8, "bdirect_256x256_w2x2"},  // 25.7, 25.1 / 27.8
-    {2048, 4096, 7168, 8, "bdirect_128x256_w1x4"},  // 39.3, 34.5 / 44.3 (64x256: 39.0, 37.3)
-    {2048, 2112, 7168, 8, "bdirect_128x256_w1x4"},  // 27.1, 27.0 / 29.7
+    // medians of 7 interleaved rounds of every configuration (us): chosen / others
+    {2048, 7168, 2048, 8, "bdirect_256x256_w2x2"},  // 26.2 / 128x256 26.6, 64x128 28.9, 64x256 29.5
+    {2048, 4096, 7168, 8, "bdirect_128x256_w1x4"},  // 35.8 / 64x256 39.7, 64x128 45.8, 256x256 47.1
+    {2048, 2112, 7168, 8, "bdirect_128x256_w1x4"},  // 28.1 / 64x128 30.9, 64x256 34.4, 256x256 42.3
 };
 
 int choose_grouped(int M, int N, int K, int E)
