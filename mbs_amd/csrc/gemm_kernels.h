@@ -242,6 +242,10 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     // Epilogue staging, per wave: 16 rows x 128 bytes (STAGE_EPI shapes).
     __shared__ __attribute__((aligned(16))) uint8_t estage[T::STAGE_EPI ? T::NW : 1][2048];
     __shared__ uint32_t ftail;   // A factor bytes of rows Mdw.. M-1 (at most 3)
+    // AFF: the unit's factors as fp32, converted once per unit from fbytes
+    // (columns: f(b); rows: f(a) * alpha), double-buffered by unit parity.
+    __shared__ __attribute__((aligned(16))) float fcolf[AFF ? 2 : 1][AFF ? T::BN : 1];
+    __shared__ __attribute__((aligned(16))) float frowf[AFF ? 2 : 1][AFF ? T::BM : 1];
     // Pair slots of the current 4-stage iteration: q0 (pair 0, stages 0-1),
     // q1 (pair 1, stages 2-3), q2 (pair 2, DMA'd by stages 0-1); pair 3 (DMA'd
     // by stages 2-3) reuses q0.  Next iteration: (q0, q1, q2) <- (q2, q0, q1).
@@ -787,6 +791,23 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                   (uint32_t)((un.e * p.N + un.n0 + k * 128) * 2 + lane * 4), go ? 0u : kOOB);
         });
     };
+    // AFF: factor bytes of the unit in fbytes[par] -> fp32 (one table lookup
+    // per row and column per unit, instead of one per element group in the
+    // epilogue, where the data-dependent table reads collide in LDS banks).
+    // Called by every thread once its unit's factor DMA is known to have
+    // landed for all waves; the epilogue reads the results after the barriers
+    // that follow.
+    auto convert_factors = [&](int par_, int m0_) __attribute__((always_inline)) {
+        if constexpr (AFF) {
+            for (int c = threadIdx.x; c < T::BN; c += T::NT) fcolf[par_][c] = ftab[fbytes[par_][256 + c]];
+            const uint32_t tail = ftail;
+            for (int r = threadIdx.x; r < T::BM; r += T::NT) {
+                const int gr = m0_ + r;
+                const uint32_t b = gr >= Mdw ? (tail >> (8 * ((gr - Mdw) & 3))) & 255u : fbytes[par_][r];
+                frowf[par_][r] = ftab[b] * p.alpha;
+            }
+        }
+    };
     factor_dma(cur, 0);
     bias_dma(cur, 0);
 
@@ -857,6 +878,9 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             stage(I0{}, FT{}, 0, post);
             stage(I1{}, FF{}, 1, post);
             stage(I2{}, FF{}, 2, false);
+            // the wait of stage 2 covers the factor DMAs issued with the
+            // previous epilogue (stage 1's may leave them in flight)
+            convert_factors(par, cur.m0);
             stage(I3{}, FF{}, 3, false);
             rotate();
         }
@@ -907,17 +931,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                 constexpr bool hf = decltype(HF)::value;
                 float fa[T::FM];
                 if constexpr (hf) {
-                    const uint32_t tail = ftail;
-                    static_for<T::FM>([&](auto i) {
-                        const int r = m0u + row_l + i * 16;
-                        const uint32_t bt = (tail >> (8 * ((r - Mdw) & 3))) & 255u;
-                        // read unconditionally: a read under the select becomes
-                        // a branch, which splits the epilogue into blocks
-                        uint32_t bd = fbytes[par][row_l + i * 16];
-                        asm volatile("" : "+v"(bd));
-                        const uint32_t b = r >= Mdw ? bt : bd;
-                        fa[i] = ftab[b] * p.alpha;
-                    });
+                    static_for<T::FM>([&](auto i) { fa[i] = frowf[par][row_l + i * 16]; });
                 }
                 // Fragment pair (j, j+1) covers 32 columns.  Lane (m, q) holds
                 // columns 4q..4q+3 of each; after two rounds of lane swaps it
@@ -931,12 +945,12 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                     PairEpi e;
                     if constexpr (hf) {
                         const int cl = wn * T::WN + j0 * 16 + q * 4;   // lane's first column in the tile
-                        const uint32_t b0 = *reinterpret_cast<const uint32_t*>(&fbytes[par][256 + cl]);
-                        const uint32_t b1 = *reinterpret_cast<const uint32_t*>(&fbytes[par][256 + cl + 16]);
+                        const f32x4 c0 = *reinterpret_cast<const f32x4*>(&fcolf[par][cl]);
+                        const f32x4 c1 = *reinterpret_cast<const f32x4*>(&fcolf[par][cl + 16]);
                         static_for<4>([&](auto K4) {
                             constexpr int k = decltype(K4)::value;
-                            e.f0[k] = ftab[(b0 >> (8 * k)) & 255];
-                            e.f1[k] = ftab[(b1 >> (8 * k)) & 255];
+                            e.f0[k] = c0[k];
+                            e.f1[k] = c1[k];
                         });
                         const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&fbias[par][cl]);
                         const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&fbias[par][cl + 16]);
