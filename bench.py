@@ -472,6 +472,35 @@ def shape_bench(M, N, K, iters):
                       "plan": mbs_amd.ext().plan_name(M, N, K), "iters": iters}), flush=True)
 
 
+def operand_data(dev, launches=100, rounds=2):
+    """configs[1]'s kernel (same plan, same instruction stream) on its own
+    operands and on operands with less bit activity: A or B or both all-zero
+    codes, and A all 1.0 codes.  Per case the phase-timer build's kernel time
+    (HIP events, eager launches) and in-kernel shader clock; the cases are
+    interleaved (order reversed in the second round), so the power
+    management's state is shared between them."""
+    import torch
+
+    M = N = K = 8192
+    (A, B, As, Bs), _ = prepare(M, N, K, 1, dev)
+    cases = [("cfg1", (A, B, As, Bs)),
+             ("A=0", (torch.zeros_like(A), B, As, Bs)),
+             ("B=0", (A, torch.zeros_like(B), As, Bs)),
+             ("A=B=0", (torch.zeros_like(A), torch.zeros_like(B), As, Bs)),
+             ("A=1.0", (torch.full_like(A, 0x22), B, As, Bs))]   # e2m1 code 2 = 1.0 in both nibbles
+    res = {}
+    for r in range(rounds):
+        for name, ops in (cases if r % 2 == 0 else cases[::-1]):
+            ph = phase_split(ops, M, N, K, launches=launches)
+            if "error" in ph:
+                return ph
+            res.setdefault(name, []).append({"kernel_us": ph["kernel_us_plain"], "sclk_mhz": ph["sclk_mhz"]})
+    flop = 2.0 * M * N * K
+    return {name: {"kernel_us": [v["kernel_us"] for v in vs], "sclk_mhz": [v["sclk_mhz"] for v in vs],
+                   "TFLOPS_best": round(flop / min(v["kernel_us"] for v in vs) / 1e6, 1)}
+            for name, vs in res.items()}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -501,6 +530,9 @@ def main():
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the graph-replayed blocks and the in-kernel clock measurement "
                          "(hardware-counter runs see only the timed launches)")
+    ap.add_argument("--operand-data", action="store_true",
+                    help="only time configs[1]'s kernel on its operands and on all-zero / "
+                         "constant operands (phase-timer build: kernel time and shader clock)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 20 device-to-device copies of MIB MiB (scales the HBM "
                          "FETCH_SIZE/WRITE_SIZE counters) and exit")
@@ -549,6 +581,9 @@ def main():
     if args.shape and not args.phase_split:
         M, N, K = (int(v) for v in args.shape.split(","))
         shape_bench(M, N, K, args.iters)
+        return
+    if args.operand_data:
+        print(json.dumps({"operand_data": operand_data(dev)}), flush=True)
         return
     if args.phase_split:
         M, N, K = (int(v) for v in args.shape.split(",")) if args.shape else (8192, 8192, 8192)
