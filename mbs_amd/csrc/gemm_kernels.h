@@ -666,7 +666,14 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         }
         static_for<NG>([&](auto G_) {
             constexpr int g = decltype(G_)::value;
-            constexpr int c = g / T::FN, j = g % T::FN;
+            // MFMA g multiplies A fragment c by B fragment j; k is its place
+            // in the fragment row.  Odd rows walk the B fragments backwards,
+            // so consecutive MFMAs always share an operand (at a row change
+            // the B fragment stays): fewer operand changes on the matrix
+            // pipe's inputs, whose switching activity sets the power-limited
+            // clock under sustained load.
+            constexpr int c = g / T::FN, k = g % T::FN;
+            constexpr int j = (c & 1) ? T::FN - 1 - k : k;
             constexpr int ar = (T::FM * u + c) & 3;
             using PKu = std::integral_constant<int, (u >> 1)>;        // pair of this stage
             using PKn = std::integral_constant<int, ((u + 1) >> 1)>;  // pair of the next
@@ -680,7 +687,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             constexpr int opb = (j & 1) + 2 * h;
             constexpr int opa = (c & 1) + 2 * h;
             // K-tail stages select scales with VALU ops: keep the wait states there.
-            if constexpr (j == 0) {
+            if constexpr (k == 0) {
                 if constexpr (first && !GEN)
                     mfma_fp4_first_w<opb, opa, nyoung>(acc[c][j], rb[u][j], ra[ar], sbv[j / 2], sav[c / 2]);
                 else
@@ -692,7 +699,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                     mfma_fp4<opb, opa, GEN>(acc[c][j], rb[u][j], ra[ar], sbv[j / 2], sav[c / 2]);
             }
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (j == 0) {
+            if constexpr (k == 0) {
                 // look-ahead A read: fragment c+2 of this stage or of the next
                 constexpr int xn = c + 2;
                 if constexpr (xn < T::FM)
