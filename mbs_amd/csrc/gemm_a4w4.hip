@@ -48,6 +48,7 @@ MBS_BDIRECT_SHAPES_A(MBS_BDIRECT_EXTERN)
 MBS_BDIRECT_SHAPES_B(MBS_BDIRECT_EXTERN)
 MBS_BDIRECT_SHAPES_C(MBS_BDIRECT_EXTERN)
 MBS_BDIRECT_SHAPES_D(MBS_BDIRECT_EXTERN)
+MBS_BDIRECT_SHAPES_E(MBS_BDIRECT_EXTERN)
 MBS_SKINNY_SHAPES(MBS_SKINNY_EXTERN)
 MBS_GROUPED_SHAPES(MBS_GROUPED_EXTERN)
 
@@ -139,6 +140,9 @@ struct Config {
     // K-tail variant
     hipError_t (*launch)(const GemmArgs&, dim3, bool, bool, hipStream_t);
     bool persistent = false;  // grid capped at the resident slots; workgroups loop over units
+    // whole K only: no K tail, no dead stages (K % 512 == 0), one split
+    // (the 32x32x64 MFMA tiles)
+    bool whole_k = false;
 };
 
 const Config kConfigs[] = {
@@ -156,6 +160,11 @@ const Config kConfigs[] = {
     {"bdirect_96x256_w1x4", kPersistent, 96, 256, 256, 1, {0.333f, 0.333f, 2.77f}, launch_bdirect<B96x256w14>, true},
     {"bdirect_64x512_w1x4", kPersistent, 64, 512, 256, 1, {0.428f, 0.428f, 3.26f}, launch_bdirect<B64x512w14>, true},
     {"bdirect_128x384_w1x4", kPersistent, 128, 384, 256, 1, {0.455f, 0.455f, 4.55f}, launch_bdirect<B128x384w14>, true},
+    // v_mfma_scale_f32_32x32x64_f8f6f4 tiles
+    {"bdirect_96x256_w1x4_m32", kPersistent, 96, 256, 256, 1, {0.333f, 0.333f, 2.77f}, launch_bdirect<B96x256m>, true, true},
+    {"bdirect_128x256_w1x4_m32", kPersistent, 128, 256, 256, 1, {0.367f, 0.367f, 3.14f}, launch_bdirect<B128x256m>, true, true},
+    {"bdirect_192x256_w1x4_m32", kPersistent, 192, 256, 256, 1, {0.467f, 0.467f, 4.17f}, launch_bdirect<B192x256m>, true, true},
+    {"bdirect_256x256_w1x4_m32", kPersistent, 256, 256, 256, 1, {0.611f, 0.611f, 7.01f}, launch_bdirect<B256x256m>, true, true},
     // skinny: bm = rows covered (16*MT), bn = B rows per workgroup (16*NF)
     // eff = streaming efficiency relative to the best variant (cold N=K=8192 timings)
     {"skinny_m16_n32_w16", kSkinny, 16, 32, 1024, 1, {0.94f, 0.f, 0.f}, launch_skinny<1, 2, 16, 4>},
@@ -219,6 +228,7 @@ bool make_plan(int config, int want_splits, int M, int N, int K, Plan* out)
         pl.grid = dim3(wgs, pl.splits, 1);
     } else {
         const int tm = (M + c.bm - 1) / c.bm, tn = (N + c.bn - 1) / c.bn;
+        if (c.whole_k && (K % 512 != 0 || want_splits > 1)) return false;
         if (want_splits <= 0) {
             // the split count the cost model prefers (workspace below 2 GiB)
             bool have = false;
@@ -294,7 +304,9 @@ double plan_cost(const Plan& pl, int M, int N, int K)
 // "a / b us" were re-measured after the epilogue stores moved to LDS staging:
 // medians of 7 interleaved rounds of the candidates, without / with MBS
 // factors (a sweep run in order is biased by the clock's response to
-// sustained load).
+// sustained load).  Entries naming an _m32 (32x32x64 MFMA) tile: medians of
+// 3 x 7 interleaved rounds against the 16x16x128 tiles, without / with
+// factors.
 struct TunedPlan {
     int M, N, K;
     const char* config;
@@ -308,11 +320,11 @@ const TunedPlan kTuned[] = {
     {256, 4096, 7168, "bdirect_64x128_w1x2", 1},  // 13.1 us
     {2048, 4096, 7168, "bdirect_128x256_w1x4", 1},  // 30.3 us
     {256, 2112, 7168, "bdirect_64x128_w1x2", 2},  // 13.1 us
-    {2048, 2112, 7168, "bdirect_128x256_w1x4", 1},  // 23.9 / 24.5 us (256x128 1x4: 25.0 / 25.8)
+    {2048, 2112, 7168, "bdirect_128x256_w1x4_m32", 1},  // 25.15 / 26.94 us (128x256 1x4: 25.72 / 26.86)
     {1000, 1280, 512, "bdirect_64x128_w1x2", 1},  // 4.9 us
     {3333, 5120, 512, "bdirect_64x128_w1x2", 1},  // 15.3 us
-    {1000, 5120, 12288, "bdirect_128x256_w1x4", 1},  // 39.1 / 38.1 us (256x128 1x4: 41.7 / 40.0)
-    {3333, 1280, 12288, "bdirect_128x256_w1x4", 1},  // 38.1 / 38.6 us (256x128 1x4: 38.9 / 39.1; 96x256: 38.4 / 38.1)
+    {1000, 5120, 12288, "bdirect_128x256_w1x4_m32", 1},  // 40.12 / 41.29 us (128x256 1x4: 41.88 / 42.72)
+    {3333, 1280, 12288, "bdirect_96x256_w1x4_m32", 1},  // 37.44 / 39.29 us (128x256 1x4: 38.69 / 39.53; 96x256: 38.81 / 39.47)
     {8192, 10240, 5120, "bdirect_256x256_w2x2", 1},  // 186.5 us
     {8192, 17408, 5120, "bdirect_192x256_w1x4", 1},  // 327.5 us
     {8192, 5120, 17408, "bdirect_256x256_w2x2", 1},  // 295.7 us
@@ -714,7 +726,8 @@ int mbs_gemm_a4w4_launch_config(int config, int splits, const uint8_t* A, const 
     Plan pl;
     if (!make_plan(config, splits, M, N, K, &pl))
         return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) + " cannot run M=" +
-                                        std::to_string(M));
+                                        std::to_string(M) + " K=" + std::to_string(K) + " with " +
+                                        std::to_string(splits) + " splits");
     return run_plan(pl, A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, scaleN_pad,
                     workspace, workspace_bytes, stream);
 }
@@ -738,7 +751,8 @@ int mbs_gemm_a4w4_launch_ex(int config, int splits, const uint8_t* A, const uint
             return fail(MBS_ERR_CONFIG, "no kernel configuration fits this problem");
     } else if (!make_plan(config, splits, M, N, K, &pl)) {
         return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) + " cannot run M=" +
-                                        std::to_string(M));
+                                        std::to_string(M) + " K=" + std::to_string(K) + " with " +
+                                        std::to_string(splits) + " splits");
     }
     return run_plan(pl, A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, scaleN_pad,
                     workspace, workspace_bytes, stream, alpha, bias);
@@ -775,12 +789,14 @@ int mbs_gemm_a4w4_launch_noalloc(int config, int splits, const uint8_t* A, const
     } else {
         if (!make_plan(config, splits, M, N, K, &pl))
             return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) + " cannot run M=" +
-                                            std::to_string(M));
+                                            std::to_string(M) + " K=" + std::to_string(K) + " with " +
+                                            std::to_string(splits) + " splits");
         // the config's own split choice falls back to no split when its
         // partials do not fit; an explicit split count is refused
         if (pl.ws_bytes > cap && splits <= 0 && !make_plan(config, 1, M, N, K, &pl))
             return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) + " cannot run M=" +
-                                            std::to_string(M));
+                                            std::to_string(M) + " K=" + std::to_string(K) + " with " +
+                                            std::to_string(splits) + " splits");
     }
     if (pl.ws_bytes > cap)
         return fail(MBS_ERR_WORKSPACE, "split-K partials need " + std::to_string(pl.ws_bytes) +

@@ -5,6 +5,8 @@
 // units, in parallel.
 #pragma once
 
+#include <type_traits>
+
 #include "mxfp4_device.h"
 #include "mbs_gemm_a4w4.h"
 
@@ -136,17 +138,30 @@ inline bool affine_epilogue(const GemmArgs& a)
 // 8 16-byte chunks stored XOR-swizzled so that the MFMA fragment reads are
 // bank-conflict free.  The epilogue turns each pair of 16-column fragments
 // into 16-byte row segments with two rounds of permlane swaps.
-template <int BM_, int BN_, int WGM_, int WGN_>
+// M32: the tile runs v_mfma_scale_f32_32x32x64_f8f6f4 (32 x 32 outputs per
+// MFMA, 64 K) instead of the 16x16x128 form.  A stage then still reads FM
+// A fragments of 1 KiB and loads FN B fragments of 1 KiB, but a fragment
+// "row" c of the stage is (K step s = c / FM32, 32-row block c32 = c %
+// FM32) and carries FN/2 MFMAs (one per 32-column block).  It covers 1x4
+// tiles with 64-column wave tiles, without K tails, K splits or groups.
+template <int BM_, int BN_, int WGM_, int WGN_, bool M32_ = false>
 struct BdShape {
     static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
+    static constexpr bool M32 = M32_;
     static constexpr int NW = WGM * WGN, NT = 64 * NW;
     static constexpr int WM = BM / WGM, WN = BN / WGN;
-    static constexpr int FM = WM / 16, FN = WN / 16;
+    static constexpr int FM = WM / 16, FN = WN / 16;    // A fragment reads, B fragment loads per stage
+    static constexpr int FM32 = WM / 32, FN32 = WN / 32;
+    static constexpr int RW = M32 ? FN / 2 : FN;        // MFMAs per fragment row
+    static constexpr int AR = M32 ? FM32 : FM, AC = M32 ? FN32 : FN;   // accumulator blocks
+    static_assert(!M32 || (WGM == 1 && WN == 64), "M32 tiles: 1xN waves, 64-column wave tiles");
     static constexpr int AF = BM / 16;                  // A fragments per stage
     // A DMAs per stage: half a pair (BM/2 rows x 128 bytes, 8 rows each),
     // DA per wave.
     static constexpr int DA = (AF + NW - 1) / NW;
-    static constexpr int SA = FM / 2, SB = FN / 2;      // scale dwords per wave per group
+    // scale dwords read per wave per 256-K group: one per 32 rows / columns
+    // (16x16x128), two per 32 rows / columns (32x32x64: combined by v_perm)
+    static constexpr int SA = M32 ? FM : FM / 2, SB = M32 ? FN : FN / 2;
     static constexpr int PSLOT = BM * 128;              // bytes of one A pair slot
     // Scales of a 256-K group: one 256-byte chunk per 32 rows (A) or columns
     // (B), gathered four chunks per 16-byte LDS DMA.
@@ -172,6 +187,9 @@ struct BdShape {
     // 2-4 workgroups per CU, store straight from registers (the staged form
     // measured 0.7-4% slower there).
     static constexpr bool STAGE_EPI = BM >= 96;
+    // epilogue staging bytes per wave: 16 rows (16x16x128) or 32 rows
+    // (32x32x64) of one 128-byte line
+    static constexpr int EPI_STAGE = M32 ? 4096 : 2048;
 };
 
 // One work unit of the persistent schedule (a tile and a K-split of it);
@@ -227,6 +245,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
 {
     static_assert(!(GROUPED && SPLIT), "grouped GEMM runs without K splits");
     static_assert(!(AFF && SPLIT), "split launches write fp32 partial sums");
+    static_assert(!T::M32 || (!GEN && !SPLIT && !GROUPED), "M32 tiles: whole-K, single-split, dense");
     __shared__ __attribute__((aligned(1024))) uint8_t pa0[T::PSLOT];
     __shared__ __attribute__((aligned(1024))) uint8_t pa1[T::PSLOT];
     __shared__ __attribute__((aligned(1024))) uint8_t pa2[T::PSLOT];
@@ -240,7 +259,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     __shared__ __attribute__((aligned(1024))) uint8_t sc1[T::SBUF];
     __shared__ float ftab[256];
     // Epilogue staging, per wave: 16 rows x 128 bytes (STAGE_EPI shapes).
-    __shared__ __attribute__((aligned(16))) uint8_t estage[T::STAGE_EPI ? T::NW : 1][2048];
+    __shared__ __attribute__((aligned(16))) uint8_t estage[T::STAGE_EPI ? T::NW : 1][T::EPI_STAGE];
     __shared__ uint32_t ftail;   // A factor bytes of rows Mdw.. M-1 (at most 3)
     // AFF: the unit's factors as fp32, converted once per unit from fbytes
     // (columns: f(b); rows: f(a) * alpha), double-buffered by unit parity.
@@ -388,16 +407,35 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         voA[d] = (uint32_t)((8 * j + (lane >> 3)) * Kp + c * 16);
     });
     // A fragment read of half h: lane L -> row L%16 of the fragment, global
-    // chunk 4h + L/16, at its swizzled position.
-    uint32_t loA[2];
-    static_for<2>([&](auto H) {
-        constexpr int h = decltype(H)::value;
-        loA[h] = (uint32_t)((lane & 15) * 128 + (((4 * h + (lane >> 4)) ^ a_swz(lane & 15)) * 16));
-    });
-    // B: the wave's fragment j is 16 rows at n0 + wn*WN + 16j.
+    // chunk 4h + L/16, at its swizzled position.  M32: of 64-K step k of the
+    // pair: lane L -> row L%32, chunk 2k + L/32.
+    uint32_t loA[T::M32 ? 4 : 2];
+    if constexpr (T::M32) {
+        static_for<4>([&](auto Kk) {
+            constexpr int k = decltype(Kk)::value;
+            loA[k] = (uint32_t)((lane & 31) * 128 + (((2 * k + (lane >> 5)) ^ a_swz(lane & 31)) * 16));
+        });
+    } else {
+        static_for<2>([&](auto H) {
+            constexpr int h = decltype(H)::value;
+            loA[h] = (uint32_t)((lane & 15) * 128 + (((4 * h + (lane >> 4)) ^ a_swz(lane & 15)) * 16));
+        });
+    }
+    // B: the wave's fragment j is 16 rows at n0 + wn*WN + 16j.  M32: fragment
+    // j = s*FN32 + j32 is the 32 rows at n0 + wn*WN + 32*j32 for 64-K step s
+    // of the stage; in the (16,16) preshuffle lane L's 16 bytes (row L%32, K
+    // bytes 32s + 16*(L/32)..) sit at 16-row group (L%32)/16, 512-byte block
+    // s, 256-byte half L/32, offset 16*(L%16).
     uint32_t voB[T::FN];
-    static_for<T::FN>([&](auto j) {
-        voB[j] = (uint32_t)((wn * T::FN + j) * K * 8 + lane * 16);
+    static_for<T::FN>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        if constexpr (T::M32) {
+            constexpr int s = j / T::FN32, j32 = j % T::FN32;
+            voB[j] = (uint32_t)((wn * T::FN + 2 * j32 + ((lane >> 4) & 1)) * K * 8 + s * 512 +
+                                (lane >> 5) * 256 + (lane & 15) * 16);
+        } else {
+            voB[j] = (uint32_t)((wn * T::FN + j) * K * 8 + lane * 16);
+        }
     });
     // Scale DMA i of this wave is the workgroup's DMA k = w + NW*i: k < NSDA
     // gathers A chunks 4k..4k+3 (lane group lane/16 -> chunk), the next NSDB
@@ -428,12 +466,22 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         dma16s(isa ? rAs : rBs, dst, voSD[i], real ? (isa ? t.as : t.bs) : kOOB);
     };
     // LDS addresses of this wave's scale dwords in each scale buffer (dword
-    // k of the A or B part at + k*256).
-    const uint32_t scA[2] = {lds_addr(sc0) + (uint32_t)((((wm * T::WM) >> 5)) * 256 + lane * 4),
-                             lds_addr(sc1) + (uint32_t)((((wm * T::WM) >> 5)) * 256 + lane * 4)};
+    // k of the A or B part at + k*256).  M32: lane L reads dwords
+    // 16*(L/32) + L%16 and 32 + that of each 32-row chunk (see scale32).
+    const uint32_t slane = T::M32 ? (uint32_t)(((lane >> 5) * 16 + (lane & 15)) * 4) : (uint32_t)(lane * 4);
+    const uint32_t scA[2] = {lds_addr(sc0) + (uint32_t)((((wm * T::WM) >> 5)) * 256) + slane,
+                             lds_addr(sc1) + (uint32_t)((((wm * T::WM) >> 5)) * 256) + slane};
     const uint32_t scB[2] = {
-        lds_addr(sc0) + (uint32_t)(T::NSDA * 1024 + ((wn * T::WN) >> 5) * 256 + lane * 4),
-        lds_addr(sc1) + (uint32_t)(T::NSDA * 1024 + ((wn * T::WN) >> 5) * 256 + lane * 4)};
+        lds_addr(sc0) + (uint32_t)(T::NSDA * 1024 + ((wn * T::WN) >> 5) * 256) + slane,
+        lds_addr(sc1) + (uint32_t)(T::NSDA * 1024 + ((wn * T::WN) >> 5) * 256) + slane};
+    // M32 scales: the four 64-K steps of a 256-K group need, in lane L, the
+    // E8M0 bytes of (row L%32, block 2k + L/32), k = 0..3.  In the shuffled
+    // layout they are bytes t and t+2 (t = (L%32)/16) of the two dwords read
+    // above; v_perm packs them so that byte k serves step k (op_sel = k).
+    const uint32_t perm_sel = ((lane >> 4) & 1) ? 0x07030501u : 0x06020400u;
+    auto scale32 = [&](int d0, int d1) __attribute__((always_inline)) {
+        return (int)__builtin_amdgcn_perm((uint32_t)d1, (uint32_t)d0, perm_sel);
+    };
     // GEN kernels also run shapes without a K tail (dead stages only).
     const bool ktail = (K & 127) != 0;
     const bool hi_lane = lane >= 32;
@@ -441,10 +489,13 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
 
     i32x4 rb[4][T::FN];     // B register ring (stage % 4)
     i32x4 ra[4];            // A fragment ring (fragment sequence % 4)
-    f32x4 acc[T::FM][T::FN];
-    static_for<T::FM>([&](auto i) {
-        static_for<T::FN>([&](auto j) { acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f}; });
+    using AccT = std::conditional_t<T::M32, f32x16, f32x4>;
+    AccT acc[T::AR][T::AC];
+    static_for<T::AR>([&](auto i) {
+        static_for<T::AC>([&](auto j) { acc[i][j] = AccT{}; });
     });
+    // M32: packed scales of the two groups in flight (set = group & 1)
+    int spa[2][T::M32 ? T::FM32 : 1], spb[2][T::M32 ? T::FN32 : 1];
 
     Unit cur = unit_of(blockIdx.x);
     Unit nxt = unit_of(blockIdx.x + G);
@@ -556,26 +607,33 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     static_assert(NI_EVEN + EPI_OPS <= 63 && NI_ODD <= 63, "vmcnt is 6 bits");
 
     // A fragment x of the wave, half H of pair K of the iteration -> ra[R].
+    // M32: fragment row x is 32-row block x % FM32 at 64-K step
+    // 2H + x / FM32 of the pair.
     auto read_a = [&](auto PK, auto H, auto X, auto R) __attribute__((always_inline)) {
-        constexpr int x = decltype(X)::value;
-        ra[decltype(R)::value] =
-            ds_read16<x * 2048>(lds_addr(qp(PK)) + loA[decltype(H)::value] + (uint32_t)(wm * T::FM * 2048));
+        constexpr int x = decltype(X)::value, h = decltype(H)::value;
+        if constexpr (T::M32)
+            ra[decltype(R)::value] = ds_read16<(x % T::FM32) * 4096>(lds_addr(qp(PK)) + loA[2 * h + x / T::FM32]);
+        else
+            ra[decltype(R)::value] =
+                ds_read16<x * 2048>(lds_addr(qp(PK)) + loA[h] + (uint32_t)(wm * T::FM * 2048));
     };
 
     // One scale dword of the group in buffer BUF -> register set SET
     // (k < SA: A dword k, else B dword k - SA).
     auto read_scale = [&](auto BUF, auto SET, auto KI) __attribute__((always_inline)) {
         constexpr int set = decltype(SET)::value, k = decltype(KI)::value, b = decltype(BUF)::value & 1;
-        if constexpr (k < T::SA) sa[set][k] = ds_read4<k * 256>(scA[b]);
-        else sb[set][k - T::SA] = ds_read4<(k - T::SA) * 256>(scB[b]);
+        constexpr int st = T::M32 ? 128 : 256;   // M32: two dwords 128 bytes apart per 32-row chunk
+        if constexpr (k < T::SA) sa[set][k] = ds_read4<k * st>(scA[b]);
+        else sb[set][k - T::SA] = ds_read4<(k - T::SA) * st>(scB[b]);
     };
     static_assert(T::FM >= 4, "the A look-ahead and scale-read schedule needs 4+ fragments");
-    // Gap of scale read k of an odd stage: spread over [FN, (FM-2)*FN), so
+    // Gap of scale read k of an odd stage: spread over [RW, (FM-2)*RW), so
     // every scale read is older than the two look-ahead fragment reads that
     // end the stage (which makes the wait of the next stage's first MFMA
-    // cover them).
+    // cover them).  RW: MFMAs (= gaps) per fragment row.
     constexpr int NSR = T::SA + T::SB;
-    constexpr auto scale_gap = [](int k) constexpr { return T::FN + (k * ((T::FM - 3) * T::FN)) / NSR; };
+    constexpr int RW = T::RW;
+    constexpr auto scale_gap = [](int k) constexpr { return RW + (k * ((T::FM - 3) * RW)) / NSR; };
     // Scale reads of an odd stage at gaps in [g0, g1).
     constexpr auto scales_in = [scale_gap](int g0, int g1) constexpr {
         int n = 0;
@@ -606,7 +664,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         constexpr int h = u & 1, sset = (u >> 1) & 1;
         constexpr int NI = ((u & 1) == 0) ? NI_EVEN : NI_ODD;   // issues of this stage
         constexpr int NIP = ((u & 1) == 0) ? NI_ODD : NI_EVEN;  // issues of the previous one
-        constexpr int NG = T::FM * T::FN;                       // MFMAs (= gaps) per stage
+        constexpr int NG = T::FM * RW;                          // MFMAs (= gaps) per stage
         // Everything issued two or more stages ago has landed (A of ls+1 for
         // this stage's look-ahead reads, B and scales of ls); the previous
         // stage's issues may still be in flight.
@@ -664,6 +722,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             static_for<T::SA>([&](auto i) { sav[i] = tail ? 0x7F7F7F7F : sav[i]; });
             static_for<T::SB>([&](auto j) { sbv[j] = tail ? 0x7F7F7F7F : sbv[j]; });
         }
+
         static_for<NG>([&](auto G_) {
             constexpr int g = decltype(G_)::value;
             // MFMA g multiplies A fragment c by B fragment j; k is its place
@@ -672,8 +731,8 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             // the B fragment stays): fewer operand changes on the matrix
             // pipe's inputs, whose switching activity sets the power-limited
             // clock under sustained load.
-            constexpr int c = g / T::FN, k = g % T::FN;
-            constexpr int j = (c & 1) ? T::FN - 1 - k : k;
+            constexpr int c = g / RW, k = g % RW;
+            constexpr int j = (c & 1) ? RW - 1 - k : k;
             constexpr int ar = (T::FM * u + c) & 3;
             using PKu = std::integral_constant<int, (u >> 1)>;        // pair of this stage
             using PKn = std::integral_constant<int, ((u + 1) >> 1)>;  // pair of the next
@@ -683,11 +742,33 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             // the chunk waits for the rest.  At c = 0 that also covers the
             // scales the stage uses (read before the look-ahead reads).
             constexpr int nyoung =
-                1 + ((u & 1) && c >= 2 ? scales_in((c - 2) * T::FN, c * T::FN) : 0);
+                1 + ((u & 1) && c >= 2 ? scales_in((c - 2) * RW, c * RW) : 0);
             constexpr int opb = (j & 1) + 2 * h;
             constexpr int opa = (c & 1) + 2 * h;
+            if constexpr (T::M32) {
+                // row c = (64-K step s of the stage, 32-row block c32); B
+                // fragment jb = (s, 32-column block j); scale byte = the step
+                // within the 256-K group.  The unit's first stage starts each
+                // accumulator at s = 0.
+                constexpr int s = c / T::FM32, c32 = c % T::FM32;
+                constexpr int kst = 2 * h + s;
+                constexpr int jb = s * T::FN32 + j;
+                constexpr bool fresh = first && s == 0;
+                const int pb = spb[sset][j], pa = spa[sset][c32];
+                if constexpr (k == 0) {
+                    if constexpr (fresh)
+                        mfma32_fp4_first_w<kst, kst, nyoung>(acc[c32][j], rb[u][jb], ra[ar], pb, pa);
+                    else
+                        mfma32_fp4_w<kst, kst, nyoung>(acc[c32][j], rb[u][jb], ra[ar], pb, pa);
+                } else {
+                    if constexpr (fresh)
+                        mfma32_fp4_first<kst, kst>(acc[c32][j], rb[u][jb], ra[ar], pb, pa);
+                    else
+                        mfma32_fp4<kst, kst>(acc[c32][j], rb[u][jb], ra[ar], pb, pa);
+                }
+            }
             // K-tail stages select scales with VALU ops: keep the wait states there.
-            if constexpr (k == 0) {
+            else if constexpr (k == 0) {
                 if constexpr (first && !GEN)
                     mfma_fp4_first_w<opb, opa, nyoung>(acc[c][j], rb[u][j], ra[ar], sbv[j / 2], sav[c / 2]);
                 else
@@ -711,11 +792,11 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                            std::integral_constant<int, xn - T::FM>{},
                            std::integral_constant<int, (T::FM * u + xn) & 3>{});
             }
-            // VMEM items over gaps [FN + FN/2, NG - FN/2)
+            // VMEM items over gaps [RW + RW/2, NG - RW/2)
             static_for<NI>([&](auto D) {
                 constexpr int d = decltype(D)::value;
-                constexpr int span = NG - 2 * T::FN > 0 ? NG - 2 * T::FN : 1;
-                constexpr int gi = T::FN + T::FN / 2 + d * span / NI;
+                constexpr int span = NG - 2 * RW > 0 ? NG - 2 * RW : 1;
+                constexpr int gi = RW + RW / 2 + d * span / NI;
                 if constexpr ((gi < NG ? gi : NG - 1) == g) issue_item(U, D, t3, ta);
             });
             // Odd stages: the next group's scale dwords (DMA'd two stages
@@ -726,6 +807,27 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                         read_scale(std::integral_constant<int, ((u + 1) >> 1) & 1>{},
                                    std::integral_constant<int, ((u + 1) >> 1) & 1>{}, KI);
                 });
+                // M32, last gap: pack the next group's scale bytes (their
+                // dwords have landed; only the two look-ahead fragment reads
+                // may still be pending), then the two wait states a VALU
+                // write needs before an MFMA reads it.
+                if constexpr (T::M32 && g == NG - 1) {
+                    constexpr int ns = ((u + 1) >> 1) & 1;
+                    wait_lgkm_for<2>(sa[ns][0]);
+                    static_for<T::SA>([&](auto i) { tie_after(sa[ns][decltype(i)::value]); });
+                    static_for<T::SB>([&](auto i) { tie_after(sb[ns][decltype(i)::value]); });
+                    static_for<T::FM32>([&](auto i) {
+                        constexpr int x = decltype(i)::value;
+                        spa[ns][x] = scale32(sa[ns][2 * x], sa[ns][2 * x + 1]);
+                    });
+                    static_for<T::FN32>([&](auto J) {
+                        constexpr int x = decltype(J)::value;
+                        spb[ns][x] = scale32(sb[ns][2 * x], sb[ns][2 * x + 1]);
+                    });
+                    static_for<T::FM32>([&](auto i) { tie_after(spa[ns][decltype(i)::value]); });
+                    static_for<T::FN32>([&](auto J) { tie_after(spb[ns][decltype(J)::value]); });
+                    asm volatile("s_nop 1");
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
         });
@@ -853,6 +955,22 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
            std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
     read_a(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{},
            std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+    if constexpr (T::M32) {   // pack group 0's scale bytes (as the odd stages do for later groups)
+        wait_lgkm_for<2>(sa[0][0]);
+        static_for<T::SA>([&](auto i) { tie_after(sa[0][decltype(i)::value]); });
+        static_for<T::SB>([&](auto i) { tie_after(sb[0][decltype(i)::value]); });
+        static_for<T::FM32>([&](auto i) {
+            constexpr int x = decltype(i)::value;
+            spa[0][x] = scale32(sa[0][2 * x], sa[0][2 * x + 1]);
+        });
+        static_for<T::FN32>([&](auto J) {
+            constexpr int x = decltype(J)::value;
+            spb[0][x] = scale32(sb[0][2 * x], sb[0][2 * x + 1]);
+        });
+        static_for<T::FM32>([&](auto i) { tie_after(spa[0][decltype(i)::value]); });
+        static_for<T::FN32>([&](auto J) { tie_after(spb[0][decltype(J)::value]); });
+        asm volatile("s_nop 1");
+    }
     if constexpr (!GEN) {
         run = target(3);
         runA = target_a(0);
@@ -907,8 +1025,8 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         barrier();
         ph.mark(kPhBar);
         mfma_drain();
-        static_for<T::FM>([&](auto i) {
-            static_for<T::FN>([&](auto j) { pin_after_drain(acc[i][j]); });
+        static_for<T::AR>([&](auto i) {
+            static_for<T::AC>([&](auto j) { pin_after_drain(acc[i][j]); });
         });
 
         // ---- epilogue of unit `cur` -------------------------------------
@@ -934,6 +1052,9 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             // bias[n], with the table and bias set up for the cases without
             // factors or bias.  Otherwise the accumulators are converted as
             // they are.
+            // (each form is defined only where it is used: their accumulator
+            // expressions do not depend on the lambdas' own parameters)
+            if constexpr (!T::M32) {
             auto epi = [&](auto HF) __attribute__((always_inline)) {
                 constexpr bool hf = decltype(HF)::value;
                 float fa[T::FM];
@@ -1083,6 +1204,67 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                 }
             };
             epi(std::integral_constant<bool, AFF>{});
+            } else {
+            // M32: acc[c32][j] of lane L holds row c32*32 + L%32 of the wave
+            // tile, columns 32j + 8q + 4v + i (q = r/4, i = r%4, v = L/32) of
+            // its 64.  One round of lane swaps (lane L <-> L+32) gives each
+            // lane 8 consecutive columns (16 bytes) of its row per column
+            // pair q, q+1; the 32 x 128-byte block goes through the wave's
+            // staging area (chunks XOR-swizzled by row) and is stored with 8
+            // neighbouring lanes per row, 4 stores per 32 rows (EPI_OPS).
+            auto epi32 = [&](auto HF) __attribute__((always_inline)) {
+                constexpr bool hf = decltype(HF)::value;
+                const int m = lane & 31, v = lane >> 5;
+                uint8_t* const stg = estage[w];
+                const int rr = lane >> 3, cc = lane & 7;
+                const int col = col_w + cc * 8;   // N % 16 == 0
+                const bool store_ok = col < p.N;
+                static_for<T::FM32>([&](auto C32) {
+                    constexpr int c32 = decltype(C32)::value;
+                    float fa = 1.0f;
+                    if constexpr (hf) fa = frowf[par][c32 * 32 + m];
+                    static_for<T::FN32>([&](auto J) {
+                        constexpr int j = decltype(J)::value;
+                        uint32_t x[4][2];   // per q: bf16 pairs of columns 32j + 8q + 4v + {0,1} / {2,3}
+                        static_for<4>([&](auto Q) {
+                            constexpr int q = decltype(Q)::value;
+                            float e[4];
+                            static_for<4>([&](auto I) { e[decltype(I)::value] = acc[c32][j][4 * q + decltype(I)::value]; });
+                            if constexpr (hf) {
+                                const int cl = wn * T::WN + 32 * j + 8 * q + 4 * v;
+                                const f32x4 f = *reinterpret_cast<const f32x4*>(&fcolf[par][cl]);
+                                const uint32_t* bw = reinterpret_cast<const uint32_t*>(&fbias[par][cl]);
+                                const uint32_t b0 = bw[0], b1 = bw[1];
+                                const float z[4] = {bf16_lo(b0), bf16_hi(b0), bf16_lo(b1), bf16_hi(b1)};
+                                static_for<4>([&](auto I) {
+                                    constexpr int i = decltype(I)::value;
+                                    e[i] = add_nc(e[i] * (fa * f[i]), z[i]);
+                                });
+                            }
+                            x[q][0] = pack_bf16x2(e[0], e[1]);
+                            x[q][1] = pack_bf16x2(e[2], e[3]);
+                        });
+                        // lanes 0-31 get columns 8q..8q+7, lanes 32-63 8(q+1)..8(q+1)+7
+                        static_for<2>([&](auto QP) {
+                            constexpr int q = 2 * decltype(QP)::value;
+                            auto s0 = __builtin_amdgcn_permlane32_swap(x[q][0], x[q + 1][0], false, false);
+                            auto s1 = __builtin_amdgcn_permlane32_swap(x[q][1], x[q + 1][1], false, false);
+                            const int chunk = 4 * j + q + v;
+                            const i32x4 val = {(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]};
+                            *reinterpret_cast<i32x4*>(stg + m * 128 + ((chunk ^ (m & 7)) * 16)) = val;
+                        });
+                    });
+                    static_for<4>([&](auto Bk) {
+                        const int r = rr + 8 * decltype(Bk)::value;
+                        const f32x4 xv = *reinterpret_cast<const f32x4*>(stg + r * 128 + ((cc ^ (r & 7)) * 16));
+                        const uint32_t o = (uint32_t)(((c32 * 32 + r) * p.N + col) * 2);
+                        store16(rO, store_ok ? o : kOOB, xv);
+                    });
+                    __builtin_amdgcn_sched_barrier(0);
+                });
+            };
+            epi32(std::integral_constant<bool, AFF>{});
+            }
         }
         ph.mark(kPhEpi);
         par ^= 1;
@@ -1248,7 +1430,12 @@ template <class T>
 hipError_t launch_bdirect(const GemmArgs& a, dim3 grid, bool gen, bool split, hipStream_t s)
 {
     const bool aff = affine_epilogue(a);
-    if (gen) {
+    if constexpr (T::M32) {
+        // whole-K, single-split plans only (make_plan offers no other)
+        if (gen || split) return hipErrorInvalidValue;
+        if (aff) hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false, false, true>), grid, dim3(T::NT), 0, s, a);
+        else hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false>), grid, dim3(T::NT), 0, s, a);
+    } else if (gen) {
         if (split) hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, true>), grid, dim3(T::NT), 0, s, a);
         else if (aff) hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false, false, true>), grid, dim3(T::NT), 0, s, a);
         else hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false>), grid, dim3(T::NT), 0, s, a);
@@ -1297,6 +1484,11 @@ using B64x512w14 = BdShape<64, 512, 1, 4>;
 using B128x384w14 = BdShape<128, 384, 1, 4>;
 using B256x128w14 = BdShape<256, 128, 1, 4>;
 using B128x256w14 = BdShape<128, 256, 1, 4>;
+// 32x32x64 MFMA tiles
+using B96x256m = BdShape<96, 256, 1, 4, true>;
+using B128x256m = BdShape<128, 256, 1, 4, true>;
+using B192x256m = BdShape<192, 256, 1, 4, true>;
+using B256x256m = BdShape<256, 256, 1, 4, true>;
 
 
 // Launcher instantiations, one translation unit per group (gemm_inst_*.hip).
@@ -1304,6 +1496,7 @@ using B128x256w14 = BdShape<128, 256, 1, 4>;
 #define MBS_BDIRECT_SHAPES_B(X) X(B64x256) X(B64x128) X(B64x64) X(B256x128w14)
 #define MBS_BDIRECT_SHAPES_C(X) X(B256x256w14) X(B192x256w14) X(B96x256w14)
 #define MBS_BDIRECT_SHAPES_D(X) X(B64x512w14) X(B128x384w14) X(B128x256w14)
+#define MBS_BDIRECT_SHAPES_E(X) X(B96x256m) X(B128x256m) X(B192x256m) X(B256x256m)
 #define MBS_GROUPED_SHAPES(X) X(B256x256) X(B128x256w14) X(B64x256) X(B64x128)
 #define MBS_SKINNY_SHAPES(X) X(1, 2, 16, 4) X(2, 2, 16, 4) X(1, 2, 8, 4) X(2, 2, 8, 4) X(1, 1, 8, 8) X(2, 1, 8, 8) X(2, 2, 4, 4)
 

@@ -17,6 +17,7 @@ typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
@@ -271,6 +272,57 @@ __device__ __forceinline__ void mfma_fp4_w(f32x4& acc, i32x4 a, i32x4 b, int sa,
     }
 }
 
+// The 32x32x64 form, v_mfma_scale_f32_32x32x64_f8f6f4 (fp4 A and B): lane L
+// supplies row L%32 of its operand with K elements 32*(L/32)..+31 (16
+// bytes) and the E8M0 scale of (row L%32, 32-K block L/32); acc[r] of lane
+// L is D[8*(r/4) + 4*(L/32) + r%4][L%32] (D = src0 x src1^T, 32 x 32 fp32).
+// OPA / OPB select the scale byte, as for the 16x16x128 form.  These
+// operands only come from loads, LDS reads and (scales) a v_perm that an
+// explicit s_nop separates from the first MFMA, so no wait states are
+// added here.
+template <int OPA, int OPB>
+__device__ __forceinline__ void mfma32_fp4_first(f32x16& acc, i32x4 a, i32x4 b, int sa, int sb)
+{
+    static_assert(OPA >= 0 && OPA < 4 && OPB >= 0 && OPB < 4, "op_sel byte index");
+    asm("v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, 0, %3, %4 op_sel:[%5,%6,0] "
+        "op_sel_hi:[%7,%8,0] cbsz:4 blgp:4"
+        : "=a"(acc)
+        : "v"(a), "v"(b), "v"(sa), "v"(sb), "n"(OPA & 1), "n"(OPB & 1), "n"(OPA >> 1),
+          "n"(OPB >> 1));
+}
+template <int OPA, int OPB>
+__device__ __forceinline__ void mfma32_fp4(f32x16& acc, i32x4 a, i32x4 b, int sa, int sb)
+{
+    static_assert(OPA >= 0 && OPA < 4 && OPB >= 0 && OPB < 4, "op_sel byte index");
+    asm("v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[%5,%6,0] "
+        "op_sel_hi:[%7,%8,0] cbsz:4 blgp:4"
+        : "+a"(acc)
+        : "v"(a), "v"(b), "v"(sa), "v"(sb), "n"(OPA & 1), "n"(OPB & 1), "n"(OPA >> 1),
+          "n"(OPB >> 1));
+}
+template <int OPA, int OPB, int W>
+__device__ __forceinline__ void mfma32_fp4_first_w(f32x16& acc, i32x4 a, i32x4 b, int sa, int sb)
+{
+    static_assert(W >= 0 && W < 16, "lgkmcnt range");
+    asm volatile("s_waitcnt lgkmcnt(%9)\n\t"
+        "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, 0, %3, %4 op_sel:[%5,%6,0] "
+        "op_sel_hi:[%7,%8,0] cbsz:4 blgp:4"
+        : "=a"(acc)
+        : "v"(a), "v"(b), "v"(sa), "v"(sb), "n"(OPA & 1), "n"(OPB & 1), "n"(OPA >> 1),
+          "n"(OPB >> 1), "n"(W));
+}
+template <int OPA, int OPB, int W>
+__device__ __forceinline__ void mfma32_fp4_w(f32x16& acc, i32x4 a, i32x4 b, int sa, int sb)
+{
+    static_assert(W >= 0 && W < 16, "lgkmcnt range");
+    asm volatile("s_waitcnt lgkmcnt(%9)\n\t"
+        "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[%5,%6,0] "
+        "op_sel_hi:[%7,%8,0] cbsz:4 blgp:4"
+        : "+a"(acc)
+        : "v"(a), "v"(b), "v"(sa), "v"(sb), "n"(OPA & 1), "n"(OPB & 1), "n"(OPA >> 1),
+          "n"(OPB >> 1), "n"(W));
+}
+
 // Wait states between the last MFMA writing an accumulator and any other
 // instruction reading it (gfx9 requires up to ~19 for a 16-pass XDL op).
 __device__ __forceinline__ void mfma_drain()
@@ -285,6 +337,10 @@ __device__ __forceinline__ void mfma_drain()
 // the drain (it cannot see the latency of an MFMA written as inline asm)
 // and read an accumulator an MFMA is still writing.
 __device__ __forceinline__ void pin_after_drain(f32x4& acc)
+{
+    asm volatile("" : "+a"(acc));
+}
+__device__ __forceinline__ void pin_after_drain(f32x16& acc)
 {
     asm volatile("" : "+a"(acc));
 }

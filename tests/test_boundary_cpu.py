@@ -183,3 +183,20 @@ def test_torch_module_rejects_host_tensors_and_bad_shapes():
     assert m.num_configs() >= 8
     assert all(m.config_name(c).startswith(("bdirect", "skinny")) for c in range(m.num_configs()))
     assert "skinny" in m.plan_name(1, 8192, 8192)
+
+
+def test_whole_k_tiles_refuse_k_tails_and_splits():
+    """The 32x32x64-MFMA tiles (configs named *_m32) run whole-K (K % 512 == 0),
+    single-split plans only: forced onto a K tail or K splits they return
+    MBS_ERR_CONFIG before any launch."""
+    L = c_lib()
+    names = [L.mbs_gemm_a4w4_config_name(i).decode() for i in range(L.mbs_gemm_a4w4_num_configs())]
+    m32 = [i for i, n in enumerate(names) if n.endswith("_m32")]
+    assert len(m32) == 4
+    for c in m32:
+        for K, splits in [(448, 1), (1536 + 64, 1), (1024, 2), (2048, 3)]:
+            snp = ((K // 32) + 7) // 8 * 8
+            st = L.mbs_gemm_a4w4_launch_config(c, splits, FAKE, FAKE, FAKE, FAKE, None, None, FAKE,
+                                               256, 256, K, 256, snp, None, 0, None)
+            assert st == 4, (names[c], K, splits)
+            assert b"cannot run" in L.mbs_last_error()

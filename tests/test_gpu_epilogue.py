@@ -8,7 +8,7 @@ import pytest
 
 import oracle
 from gpu_util import Case, assert_close, bf16_to_f32, say
-from test_gpu_gemm import config_name, configs_for
+from test_gpu_gemm import config_name, configs_for, split_counts
 
 pytestmark = pytest.mark.gpu
 
@@ -39,8 +39,8 @@ def test_affine_epilogue_every_config(dev, M, N, K, factors):
     ref = oracle.bf16_bits_to_f32(oracle.epilogue_affine_bf16(
         c32.astype(np.float32), af if factors else None, bf if factors else None, 0.75, bias))
     m = mbs_amd.ext()
-    for cfg in configs_for(M):
-        for splits in (1, 2):
+    for cfg in configs_for(M, K):
+        for splits in split_counts(cfg, (1, 2)):
             say(f"affine M={M} N={N} K={K} factors={factors} config={config_name(cfg)} splits={splits}")
             args = (case.A, case.B, case.As, case.Bs, case.Af, case.Bf)
             plain = m.gemm_a4w4_config(cfg, splits, *args)

@@ -30,9 +30,20 @@ def config_name(c):
     return mbs_amd.ext().config_name(c)
 
 
-def configs_for(M):
-    return [c for c in range(n_configs()) if not (config_name(c).startswith("skinny") and
-                                                  M > (16 if "m16" in config_name(c) else 32))]
+def whole_k_only(c):
+    """The 32x32x64-MFMA tiles run whole-K (K % 512 == 0), single-split plans."""
+    return config_name(c).endswith("_m32")
+
+
+def configs_for(M, K):
+    """Configurations that take M rows (decode kernels up to their M) and K."""
+    return [c for c in range(n_configs())
+            if not (config_name(c).startswith("skinny") and M > (16 if "m16" in config_name(c) else 32))
+            and not (whole_k_only(c) and K % 512)]
+
+
+def split_counts(c, counts):
+    return (1,) if whole_k_only(c) else counts
 
 
 def ones(R, K):
@@ -70,7 +81,7 @@ def test_one_hot_products(dev):
         b = np.zeros((N, K // 2), np.uint8)
         a[m, k // 2] = 0x4 << (4 * (k % 2))
         b[n, k // 2] = 0x5 << (4 * (k % 2))
-        for cfg in configs_for(M):
+        for cfg in configs_for(M, K):
             out = bf16_to_f32(Case(a, s, b, s).run(config=cfg))[:M]
             exp = np.zeros((M, N), np.float32)
             exp[m, n] = 6.0
@@ -91,8 +102,8 @@ def test_golden_cfg0_every_config(dev, gold, factors):
     M = c.M
     say(f"golden cfg0 factors={factors} default plan")
     assert_close(bf16_to_f32(c.run())[:M], ref, "default plan")
-    for cfg in configs_for(M):
-        for splits in (1, 2):
+    for cfg in configs_for(M, c.K):
+        for splits in split_counts(cfg, (1, 2)):
             say(f"golden cfg0 factors={factors} config={config_name(cfg)} splits={splits}")
             got = bf16_to_f32(c.run(config=cfg, splits=splits))[:M]
             assert_close(got, ref, f"{config_name(cfg)} splits={splits}")
@@ -122,8 +133,8 @@ def test_ragged_every_config(dev, M, N, K):
         ref = oracle.bf16_bits_to_f32(c.reference())
         say(f"ragged M={M} N={N} K={K} factors={factors} default")
         assert_close(bf16_to_f32(c.run())[:M], ref, "default plan")
-        for cfg in configs_for(M):
-            for splits in (1, 3):
+        for cfg in configs_for(M, K):
+            for splits in split_counts(cfg, (1, 3)):
                 say(f"ragged M={M} N={N} K={K} factors={factors} {config_name(cfg)} s={splits}")
                 got = bf16_to_f32(c.run(config=cfg, splits=splits))[:M]
                 assert_close(got, ref, f"{config_name(cfg)} splits={splits}")
@@ -135,8 +146,8 @@ def test_padding_rows_untouched_and_deterministic(dev):
     rng = np.random.default_rng(2)
     M, N, K = 45, 96, 512
     c = rand_case(rng, M, N, K, factors=True)
-    for cfg in [None] + configs_for(M):
-        for splits in (1, 2):
+    for cfg in [None] + configs_for(M, K):
+        for splits in (1,) if cfg is None else split_counts(cfg, (1, 2)):
             say(f"padding rows config={cfg} splits={splits}")
             out = torch.full((c.Mpad, N), 7.0, dtype=torch.bfloat16, device=c.A.device)
             out = c.run(config=cfg, splits=splits, out=out)
@@ -167,7 +178,7 @@ def test_edge_scales(dev):
     c = Case(xp, xs, wp, ws)
     ref = oracle.bf16_bits_to_f32(c.reference())
     assert np.all(np.isnan(ref[11]))
-    for cfg in [None] + configs_for(M):
+    for cfg in [None] + configs_for(M, K):
         say(f"edge scales config={cfg}")
         got = bf16_to_f32(c.run(config=cfg) if cfg is not None else c.run())[:M]
         assert_close(got, ref, f"config {cfg}")
