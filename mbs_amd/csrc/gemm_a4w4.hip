@@ -316,15 +316,15 @@ const TunedPlan kTuned[] = {
     {1024, 17408, 5120, "bdirect_128x384_w1x4", 1},  // 54.6-55.3 us (192x256: 56.6-57.9)
     {1024, 1024, 5120, "bdirect_64x128_w1x2", 1},  // 10.7 us
     {256, 7168, 2048, "bdirect_64x128_w1x2", 1},  // 7.1 us
-    {2048, 7168, 2048, "bdirect_256x256_w1x4", 1},  // 20.2 / 22.3 us (256x256 2x2: 20.9 / 22.4)
+    {2048, 7168, 2048, "bdirect_256x256_w1x4", 1},  // 22.04 / 23.85 us (2x2: 22.78 / 24.38; 256x256 1x4 m32: 22.03 / 23.95)
     {256, 4096, 7168, "bdirect_64x128_w1x2", 1},  // 13.1 us
-    {2048, 4096, 7168, "bdirect_128x256_w1x4", 1},  // 30.3 us
+    {2048, 4096, 7168, "bdirect_128x256_w1x4_m32", 1},  // 33.38 / 34.62 us (128x256 1x4: 34.40 / 34.94)
     {256, 2112, 7168, "bdirect_64x128_w1x2", 2},  // 13.1 us
-    {2048, 2112, 7168, "bdirect_128x256_w1x4_m32", 1},  // 25.15 / 26.94 us (128x256 1x4: 25.72 / 26.86)
+    {2048, 2112, 7168, "bdirect_128x256_w1x4_m32", 1},  // 24.89 / 26.10 us (128x256 1x4: 25.78 / 27.05)
     {1000, 1280, 512, "bdirect_64x128_w1x2", 1},  // 4.9 us
     {3333, 5120, 512, "bdirect_64x128_w1x2", 1},  // 15.3 us
-    {1000, 5120, 12288, "bdirect_128x256_w1x4_m32", 1},  // 40.12 / 41.29 us (128x256 1x4: 41.88 / 42.72)
-    {3333, 1280, 12288, "bdirect_96x256_w1x4_m32", 1},  // 37.44 / 39.29 us (128x256 1x4: 38.69 / 39.53; 96x256: 38.81 / 39.47)
+    {1000, 5120, 12288, "bdirect_128x256_w1x4_m32", 1},  // 40.01 / 40.32 us (128x256 1x4: 41.74 / 42.37)
+    {3333, 1280, 12288, "bdirect_96x256_w1x4_m32", 1},  // 37.53 / 38.45 us (128x256 1x4: 38.41 / 39.28; 96x256: 39.60 / 39.90)
     {8192, 10240, 5120, "bdirect_256x256_w2x2", 1},  // 186.5 us
     {8192, 17408, 5120, "bdirect_192x256_w1x4", 1},  // 327.5 us
     {8192, 5120, 17408, "bdirect_256x256_w2x2", 1},  // 295.7 us

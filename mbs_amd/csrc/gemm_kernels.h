@@ -1219,6 +1219,22 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                 const int rr = lane >> 3, cc = lane & 7;
                 const int col = col_w + cc * 8;   // N % 16 == 0
                 const bool store_ok = col < p.N;
+                // the lane's column factors and bias words, read once for all
+                // row blocks: columns 32j + 8q + 4v .. +3
+                f32x4 fcol[hf ? T::FN32 : 1][hf ? 4 : 1];
+                uint32_t zw[hf ? T::FN32 : 1][hf ? 4 : 1][2];
+                if constexpr (hf) {
+                    static_for<T::FN32>([&](auto J) {
+                        static_for<4>([&](auto Q) {
+                            constexpr int j = decltype(J)::value, q = decltype(Q)::value;
+                            const int cl = wn * T::WN + 32 * j + 8 * q + 4 * v;
+                            fcol[j][q] = *reinterpret_cast<const f32x4*>(&fcolf[par][cl]);
+                            const uint32_t* bw = reinterpret_cast<const uint32_t*>(&fbias[par][cl]);
+                            zw[j][q][0] = bw[0];
+                            zw[j][q][1] = bw[1];
+                        });
+                    });
+                }
                 static_for<T::FM32>([&](auto C32) {
                     constexpr int c32 = decltype(C32)::value;
                     float fa = 1.0f;
@@ -1231,10 +1247,8 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                             float e[4];
                             static_for<4>([&](auto I) { e[decltype(I)::value] = acc[c32][j][4 * q + decltype(I)::value]; });
                             if constexpr (hf) {
-                                const int cl = wn * T::WN + 32 * j + 8 * q + 4 * v;
-                                const f32x4 f = *reinterpret_cast<const f32x4*>(&fcolf[par][cl]);
-                                const uint32_t* bw = reinterpret_cast<const uint32_t*>(&fbias[par][cl]);
-                                const uint32_t b0 = bw[0], b1 = bw[1];
+                                const f32x4 f = fcol[j][q];
+                                const uint32_t b0 = zw[j][q][0], b1 = zw[j][q][1];
                                 const float z[4] = {bf16_lo(b0), bf16_hi(b0), bf16_lo(b1), bf16_hi(b1)};
                                 static_for<4>([&](auto I) {
                                     constexpr int i = decltype(I)::value;
