@@ -165,6 +165,7 @@ const Config kConfigs[] = {
     {"bdirect_128x256_w1x4_m32", kPersistent, 128, 256, 256, 1, {0.367f, 0.367f, 3.14f}, launch_bdirect<B128x256m>, true, true},
     {"bdirect_192x256_w1x4_m32", kPersistent, 192, 256, 256, 1, {0.467f, 0.467f, 4.17f}, launch_bdirect<B192x256m>, true, true},
     {"bdirect_256x256_w1x4_m32", kPersistent, 256, 256, 256, 1, {0.611f, 0.611f, 7.01f}, launch_bdirect<B256x256m>, true, true},
+    {"bdirect_128x384_w1x4_m32", kPersistent, 128, 384, 256, 1, {0.455f, 0.455f, 4.55f}, launch_bdirect<B128x384m>, true, true},
     // skinny: bm = rows covered (16*MT), bn = B rows per workgroup (16*NF)
     // eff = streaming efficiency relative to the best variant (cold N=K=8192 timings)
     {"skinny_m16_n32_w16", kSkinny, 16, 32, 1024, 1, {0.94f, 0.f, 0.f}, launch_skinny<1, 2, 16, 4>},
@@ -313,7 +314,7 @@ struct TunedPlan {
     int splits;
 };
 const TunedPlan kTuned[] = {
-    {1024, 17408, 5120, "bdirect_128x384_w1x4", 1},  // 54.6-55.3 us (192x256: 56.6-57.9)
+    {1024, 17408, 5120, "bdirect_128x384_w1x4_m32", 1},  // 50.41 / 53.84 us (128x384 1x4: 51.80 / 54.15)
     {1024, 1024, 5120, "bdirect_64x128_w1x2", 1},  // 10.7 us
     {256, 7168, 2048, "bdirect_64x128_w1x2", 1},  // 7.1 us
     {2048, 7168, 2048, "bdirect_256x256_w1x4", 1},  // 22.04 / 23.85 us (2x2: 22.78 / 24.38; 256x256 1x4 m32: 22.03 / 23.95)

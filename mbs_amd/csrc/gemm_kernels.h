@@ -143,7 +143,7 @@ inline bool affine_epilogue(const GemmArgs& a)
 // A fragments of 1 KiB and loads FN B fragments of 1 KiB, but a fragment
 // "row" c of the stage is (K step s = c / FM32, 32-row block c32 = c %
 // FM32) and carries FN/2 MFMAs (one per 32-column block).  It covers 1x4
-// tiles with 64-column wave tiles, without K tails, K splits or groups.
+// tiles with 64- or 96-column wave tiles, without K tails, K splits or groups.
 template <int BM_, int BN_, int WGM_, int WGN_, bool M32_ = false>
 struct BdShape {
     static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
@@ -154,7 +154,7 @@ struct BdShape {
     static constexpr int FM32 = WM / 32, FN32 = WN / 32;
     static constexpr int RW = M32 ? FN / 2 : FN;        // MFMAs per fragment row
     static constexpr int AR = M32 ? FM32 : FM, AC = M32 ? FN32 : FN;   // accumulator blocks
-    static_assert(!M32 || (WGM == 1 && WN == 64), "M32 tiles: 1xN waves, 64-column wave tiles");
+    static_assert(!M32 || (WGM == 1 && (WN == 64 || WN == 96)), "M32 tiles: 1xN waves, 64 or 96 columns per wave");
     static constexpr int AF = BM / 16;                  // A fragments per stage
     // A DMAs per stage: half a pair (BM/2 rows x 128 bytes, 8 rows each),
     // DA per wave.
@@ -1206,19 +1206,20 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             epi(std::integral_constant<bool, AFF>{});
             } else {
             // M32: acc[c32][j] of lane L holds row c32*32 + L%32 of the wave
-            // tile, columns 32j + 8q + 4v + i (q = r/4, i = r%4, v = L/32) of
-            // its 64.  One round of lane swaps (lane L <-> L+32) gives each
-            // lane 8 consecutive columns (16 bytes) of its row per column
-            // pair q, q+1; the 32 x 128-byte block goes through the wave's
-            // staging area (chunks XOR-swizzled by row) and is stored with 8
-            // neighbouring lanes per row, 4 stores per 32 rows (EPI_OPS).
+            // tile, columns 32j + 8q + 4v + i (q = r/4, i = r%4, v = L/32).
+            // One round of lane swaps (lane L <-> L+32) gives each lane 8
+            // consecutive columns (16 bytes) of its row per column pair q,
+            // q+1.  Each pair of 32-column blocks (a 128-byte line of 32
+            // rows) goes through the wave's staging area, chunks XOR-swizzled
+            // by row, and is stored with 8 neighbouring lanes per row: 4
+            // stores per 32 rows.  A trailing single block (96-column wave
+            // tiles) is staged as 32 x 64 bytes and stored with 4 lanes per
+            // row: 2 stores.  Together FM * (FN / 2) stores (EPI_OPS).
             auto epi32 = [&](auto HF) __attribute__((always_inline)) {
                 constexpr bool hf = decltype(HF)::value;
+                constexpr int NL = T::FN32 / 2;   // whole 128-byte lines
                 const int m = lane & 31, v = lane >> 5;
                 uint8_t* const stg = estage[w];
-                const int rr = lane >> 3, cc = lane & 7;
-                const int col = col_w + cc * 8;   // N % 16 == 0
-                const bool store_ok = col < p.N;
                 // the lane's column factors and bias words, read once for all
                 // row blocks: columns 32j + 8q + 4v .. +3
                 f32x4 fcol[hf ? T::FN32 : 1][hf ? 4 : 1];
@@ -1235,45 +1236,79 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                         });
                     });
                 }
+                // bf16 of block (c32, j) after the lane swaps: piece[h] holds
+                // 16-byte chunk 2h + v of the block's 64 bytes in the lane's row
+                auto block_bits = [&](auto C32, auto J, float fa, i32x4 (&piece)[2])
+                    __attribute__((always_inline)) {
+                    constexpr int c32 = decltype(C32)::value, j = decltype(J)::value;
+                    uint32_t x[4][2];   // per q: bf16 pairs of columns 32j + 8q + 4v + {0,1} / {2,3}
+                    static_for<4>([&](auto Q) {
+                        constexpr int q = decltype(Q)::value;
+                        float e[4];
+                        static_for<4>([&](auto I) { e[decltype(I)::value] = acc[c32][j][4 * q + decltype(I)::value]; });
+                        if constexpr (hf) {
+                            const f32x4 f = fcol[j][q];
+                            const uint32_t b0 = zw[j][q][0], b1 = zw[j][q][1];
+                            const float z[4] = {bf16_lo(b0), bf16_hi(b0), bf16_lo(b1), bf16_hi(b1)};
+                            static_for<4>([&](auto I) {
+                                constexpr int i = decltype(I)::value;
+                                e[i] = add_nc(e[i] * (fa * f[i]), z[i]);
+                            });
+                        }
+                        x[q][0] = pack_bf16x2(e[0], e[1]);
+                        x[q][1] = pack_bf16x2(e[2], e[3]);
+                    });
+                    // lanes 0-31 get columns 8q..8q+7, lanes 32-63 8(q+1)..8(q+1)+7
+                    static_for<2>([&](auto H2) {
+                        constexpr int q = 2 * decltype(H2)::value;
+                        auto s0 = __builtin_amdgcn_permlane32_swap(x[q][0], x[q + 1][0], false, false);
+                        auto s1 = __builtin_amdgcn_permlane32_swap(x[q][1], x[q + 1][1], false, false);
+                        piece[decltype(H2)::value] = i32x4{(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]};
+                    });
+                };
                 static_for<T::FM32>([&](auto C32) {
                     constexpr int c32 = decltype(C32)::value;
                     float fa = 1.0f;
                     if constexpr (hf) fa = frowf[par][c32 * 32 + m];
-                    static_for<T::FN32>([&](auto J) {
-                        constexpr int j = decltype(J)::value;
-                        uint32_t x[4][2];   // per q: bf16 pairs of columns 32j + 8q + 4v + {0,1} / {2,3}
-                        static_for<4>([&](auto Q) {
-                            constexpr int q = decltype(Q)::value;
-                            float e[4];
-                            static_for<4>([&](auto I) { e[decltype(I)::value] = acc[c32][j][4 * q + decltype(I)::value]; });
-                            if constexpr (hf) {
-                                const f32x4 f = fcol[j][q];
-                                const uint32_t b0 = zw[j][q][0], b1 = zw[j][q][1];
-                                const float z[4] = {bf16_lo(b0), bf16_hi(b0), bf16_lo(b1), bf16_hi(b1)};
-                                static_for<4>([&](auto I) {
-                                    constexpr int i = decltype(I)::value;
-                                    e[i] = add_nc(e[i] * (fa * f[i]), z[i]);
-                                });
-                            }
-                            x[q][0] = pack_bf16x2(e[0], e[1]);
-                            x[q][1] = pack_bf16x2(e[2], e[3]);
+                    static_for<NL>([&](auto Ln) {
+                        constexpr int ln = decltype(Ln)::value;
+                        static_for<2>([&](auto J2) {
+                            constexpr int jj = decltype(J2)::value;
+                            i32x4 piece[2];
+                            block_bits(C32, std::integral_constant<int, 2 * ln + jj>{}, fa, piece);
+                            static_for<2>([&](auto H2) {
+                                const int chunk = 4 * jj + 2 * decltype(H2)::value + v;
+                                *reinterpret_cast<i32x4*>(stg + m * 128 + ((chunk ^ (m & 7)) * 16)) =
+                                    piece[decltype(H2)::value];
+                            });
                         });
-                        // lanes 0-31 get columns 8q..8q+7, lanes 32-63 8(q+1)..8(q+1)+7
-                        static_for<2>([&](auto QP) {
-                            constexpr int q = 2 * decltype(QP)::value;
-                            auto s0 = __builtin_amdgcn_permlane32_swap(x[q][0], x[q + 1][0], false, false);
-                            auto s1 = __builtin_amdgcn_permlane32_swap(x[q][1], x[q + 1][1], false, false);
-                            const int chunk = 4 * j + q + v;
-                            const i32x4 val = {(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]};
-                            *reinterpret_cast<i32x4*>(stg + m * 128 + ((chunk ^ (m & 7)) * 16)) = val;
+                        const int rr = lane >> 3, cc = lane & 7;
+                        const int col = col_w + ln * 64 + cc * 8;   // N % 16 == 0
+                        static_for<4>([&](auto Bk) {
+                            const int r = rr + 8 * decltype(Bk)::value;
+                            const f32x4 xv = *reinterpret_cast<const f32x4*>(stg + r * 128 + ((cc ^ (r & 7)) * 16));
+                            const uint32_t o = (uint32_t)(((c32 * 32 + r) * p.N + col) * 2);
+                            store16(rO, col < p.N ? o : kOOB, xv);
                         });
                     });
-                    static_for<4>([&](auto Bk) {
-                        const int r = rr + 8 * decltype(Bk)::value;
-                        const f32x4 xv = *reinterpret_cast<const f32x4*>(stg + r * 128 + ((cc ^ (r & 7)) * 16));
-                        const uint32_t o = (uint32_t)(((c32 * 32 + r) * p.N + col) * 2);
-                        store16(rO, store_ok ? o : kOOB, xv);
-                    });
+                    if constexpr (T::FN32 % 2 == 1) {
+                        i32x4 piece[2];
+                        block_bits(C32, std::integral_constant<int, T::FN32 - 1>{}, fa, piece);
+                        static_for<2>([&](auto H2) {
+                            const int chunk = 2 * decltype(H2)::value + v;
+                            *reinterpret_cast<i32x4*>(stg + m * 64 + ((chunk ^ ((m >> 1) & 3)) * 16)) =
+                                piece[decltype(H2)::value];
+                        });
+                        const int rr = lane >> 2, cc = lane & 3;
+                        const int col = col_w + NL * 64 + cc * 8;
+                        static_for<2>([&](auto Bk) {
+                            const int r = rr + 16 * decltype(Bk)::value;
+                            const f32x4 xv =
+                                *reinterpret_cast<const f32x4*>(stg + r * 64 + ((cc ^ ((r >> 1) & 3)) * 16));
+                            const uint32_t o = (uint32_t)(((c32 * 32 + r) * p.N + col) * 2);
+                            store16(rO, col < p.N ? o : kOOB, xv);
+                        });
+                    }
                     __builtin_amdgcn_sched_barrier(0);
                 });
             };
@@ -1503,6 +1538,7 @@ using B96x256m = BdShape<96, 256, 1, 4, true>;
 using B128x256m = BdShape<128, 256, 1, 4, true>;
 using B192x256m = BdShape<192, 256, 1, 4, true>;
 using B256x256m = BdShape<256, 256, 1, 4, true>;
+using B128x384m = BdShape<128, 384, 1, 4, true>;
 
 
 // Launcher instantiations, one translation unit per group (gemm_inst_*.hip).
@@ -1510,7 +1546,7 @@ using B256x256m = BdShape<256, 256, 1, 4, true>;
 #define MBS_BDIRECT_SHAPES_B(X) X(B64x256) X(B64x128) X(B64x64) X(B256x128w14)
 #define MBS_BDIRECT_SHAPES_C(X) X(B256x256w14) X(B192x256w14) X(B96x256w14)
 #define MBS_BDIRECT_SHAPES_D(X) X(B64x512w14) X(B128x384w14) X(B128x256w14)
-#define MBS_BDIRECT_SHAPES_E(X) X(B96x256m) X(B128x256m) X(B192x256m) X(B256x256m)
+#define MBS_BDIRECT_SHAPES_E(X) X(B96x256m) X(B128x256m) X(B192x256m) X(B256x256m) X(B128x384m)
 #define MBS_GROUPED_SHAPES(X) X(B256x256) X(B128x256w14) X(B64x256) X(B64x128)
 #define MBS_SKINNY_SHAPES(X) X(1, 2, 16, 4) X(2, 2, 16, 4) X(1, 2, 8, 4) X(2, 2, 8, 4) X(1, 1, 8, 8) X(2, 1, 8, 8) X(2, 2, 4, 4)
 

@@ -192,7 +192,7 @@ def test_whole_k_tiles_refuse_k_tails_and_splits():
     L = c_lib()
     names = [L.mbs_gemm_a4w4_config_name(i).decode() for i in range(L.mbs_gemm_a4w4_num_configs())]
     m32 = [i for i, n in enumerate(names) if n.endswith("_m32")]
-    assert len(m32) == 4
+    assert len(m32) == 5
     for c in m32:
         for K, splits in [(448, 1), (1536 + 64, 1), (1024, 2), (2048, 3)]:
             snp = ((K // 32) + 7) // 8 * 8
