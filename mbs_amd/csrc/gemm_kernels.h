@@ -468,12 +468,12 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     // LDS addresses of this wave's scale dwords in each scale buffer (dword
     // k of the A or B part at + k*256).  M32: lane L reads dwords
     // 16*(L/32) + L%16 and 32 + that of each 32-row chunk (see scale32).
-    const uint32_t slane = T::M32 ? (uint32_t)(((lane >> 5) * 16 + (lane & 15)) * 4) : (uint32_t)(lane * 4);
-    const uint32_t scA[2] = {lds_addr(sc0) + (uint32_t)((((wm * T::WM) >> 5)) * 256) + slane,
-                             lds_addr(sc1) + (uint32_t)((((wm * T::WM) >> 5)) * 256) + slane};
+    const int slane = T::M32 ? ((lane >> 5) * 16 + (lane & 15)) * 4 : lane * 4;
+    const uint32_t scA[2] = {lds_addr(sc0) + (uint32_t)((((wm * T::WM) >> 5)) * 256 + slane),
+                             lds_addr(sc1) + (uint32_t)((((wm * T::WM) >> 5)) * 256 + slane)};
     const uint32_t scB[2] = {
-        lds_addr(sc0) + (uint32_t)(T::NSDA * 1024 + ((wn * T::WN) >> 5) * 256) + slane,
-        lds_addr(sc1) + (uint32_t)(T::NSDA * 1024 + ((wn * T::WN) >> 5) * 256) + slane};
+        lds_addr(sc0) + (uint32_t)(T::NSDA * 1024 + ((wn * T::WN) >> 5) * 256 + slane),
+        lds_addr(sc1) + (uint32_t)(T::NSDA * 1024 + ((wn * T::WN) >> 5) * 256 + slane)};
     // M32 scales: the four 64-K steps of a 256-K group need, in lane L, the
     // E8M0 bytes of (row L%32, block 2k + L/32), k = 0..3.  In the shuffled
     // layout they are bytes t and t+2 (t = (L%32)/16) of the two dwords read
