@@ -40,7 +40,7 @@ ARCH = "gfx950"
 # (gemm_inst_*.hip) so that they compile in parallel.
 HIP_SOURCES = [
     "gemm_inst_bdirect_c.hip", "gemm_inst_bdirect_d.hip", "gemm_inst_bdirect_e.hip", "gemm_inst_bdirect_a.hip",
-    "gemm_inst_bdirect_b.hip", "gemm_inst_grouped.hip",
+    "gemm_inst_bdirect_b.hip", "gemm_inst_grouped.hip", "gemm_inst_grouped_m.hip",
     "gemm_inst_skinny.hip",
     "gemm_a4w4.hip", "mxfp4_format.hip",
 ]

@@ -51,6 +51,7 @@ MBS_BDIRECT_SHAPES_D(MBS_BDIRECT_EXTERN)
 MBS_BDIRECT_SHAPES_E(MBS_BDIRECT_EXTERN)
 MBS_SKINNY_SHAPES(MBS_SKINNY_EXTERN)
 MBS_GROUPED_SHAPES(MBS_GROUPED_EXTERN)
+MBS_GROUPED_SHAPES_M(MBS_GROUPED_EXTERN)
 
 // ======================================================================
 // Split-K reduction: out[m][n..n+3] = epilogue(sum_s ws[s][m][n..n+3])
@@ -477,6 +478,9 @@ const GroupedConfig kGrouped[] = {
     {"bdirect_128x256_w1x4", launch_bdirect_grouped<B128x256w14>},
     {"bdirect_64x256_w1x4", launch_bdirect_grouped<B64x256>},
     {"bdirect_64x128_w1x2", launch_bdirect_grouped<B64x128>},
+    // 32x32x64-MFMA tiles: whole-K plans only (K % 512 == 0)
+    {"bdirect_128x256_w1x4_m32", launch_bdirect_grouped<B128x256m>},
+    {"bdirect_256x256_w1x4_m32", launch_bdirect_grouped<B256x256m>},
 };
 constexpr int kNumGrouped = (int)(sizeof(kGrouped) / sizeof(kGrouped[0]));
 
@@ -498,9 +502,9 @@ struct TunedGrouped {
 };
 const TunedGrouped kTunedGrouped[] = {
     // medians of 7 interleaved rounds of every configuration (us): chosen / others
-    {2048, 7168, 2048, 8, "bdirect_256x256_w2x2"},  // 26.2 / 128x256 26.6, 64x128 28.9, 64x256 29.5
-    {2048, 4096, 7168, 8, "bdirect_128x256_w1x4"},  // 35.8 / 64x256 39.7, 64x128 45.8, 256x256 47.1
-    {2048, 2112, 7168, 8, "bdirect_128x256_w1x4"},  // 28.1 / 64x128 30.9, 64x256 34.4, 256x256 42.3
+    {2048, 7168, 2048, 8, "bdirect_256x256_w1x4_m32"},  // 24.8 / 256x256 2x2 25.4, 128x256 26.1, m32 128x256 27.6
+    {2048, 4096, 7168, 8, "bdirect_128x256_w1x4"},  // 34.3 / 64x256 39.1, m32 128x256 39.3, m32 256x256 44.5
+    {2048, 2112, 7168, 8, "bdirect_128x256_w1x4_m32"},  // 26.2 / 128x256 27.1, 64x128 29.6, 64x256 33.5
 };
 
 int choose_grouped(int M, int N, int K, int E)
@@ -531,6 +535,9 @@ int run_grouped(int g, const uint8_t* A, const uint8_t* B, const uint8_t* As, co
                 int N, int K, int snp, void* stream, float alpha, const void* bias)
 {
     const Config& c = kConfigs[config_index(kGrouped[g].dense)];
+    if (c.whole_k && K % 512 != 0)
+        return fail(MBS_ERR_CONFIG, std::string(c.name) + " cannot run K=" + std::to_string(K) +
+                                        " (whole-K tiles need K % 512 == 0)");
     GemmArgs a{};
     a.A = A; a.B = B; a.As = As; a.Bs = Bs; a.Af = Af; a.Bf = Bf;
     a.out = static_cast<uint16_t*>(out);

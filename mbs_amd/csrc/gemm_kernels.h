@@ -245,7 +245,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
 {
     static_assert(!(GROUPED && SPLIT), "grouped GEMM runs without K splits");
     static_assert(!(AFF && SPLIT), "split launches write fp32 partial sums");
-    static_assert(!T::M32 || (!GEN && !SPLIT && !GROUPED), "M32 tiles: whole-K, single-split, dense");
+    static_assert(!T::M32 || (!GEN && !SPLIT), "M32 tiles: whole-K, single-split");
     __shared__ __attribute__((aligned(1024))) uint8_t pa0[T::PSLOT];
     __shared__ __attribute__((aligned(1024))) uint8_t pa1[T::PSLOT];
     __shared__ __attribute__((aligned(1024))) uint8_t pa2[T::PSLOT];
@@ -1501,7 +1501,12 @@ template <class T>
 hipError_t launch_bdirect_grouped(const GemmArgs& a, dim3 grid, bool gen, bool, hipStream_t s)
 {
     const bool aff = affine_epilogue(a);
-    if (gen) {
+    if constexpr (T::M32) {
+        // whole-K plans only (run_grouped refuses K % 512 != 0)
+        if (gen) return hipErrorInvalidValue;
+        if (aff) hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false, true, true>), grid, dim3(T::NT), 0, s, a);
+        else hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false, true>), grid, dim3(T::NT), 0, s, a);
+    } else if (gen) {
         if (aff) hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false, true, true>), grid, dim3(T::NT), 0, s, a);
         else hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false, true>), grid, dim3(T::NT), 0, s, a);
     } else {
@@ -1548,6 +1553,7 @@ using B128x384m = BdShape<128, 384, 1, 4, true>;
 #define MBS_BDIRECT_SHAPES_D(X) X(B64x512w14) X(B128x384w14) X(B128x256w14)
 #define MBS_BDIRECT_SHAPES_E(X) X(B96x256m) X(B128x256m) X(B192x256m) X(B256x256m) X(B128x384m)
 #define MBS_GROUPED_SHAPES(X) X(B256x256) X(B128x256w14) X(B64x256) X(B64x128)
+#define MBS_GROUPED_SHAPES_M(X) X(B128x256m) X(B256x256m)
 #define MBS_SKINNY_SHAPES(X) X(1, 2, 16, 4) X(2, 2, 16, 4) X(1, 2, 8, 4) X(2, 2, 8, 4) X(1, 1, 8, 8) X(2, 1, 8, 8) X(2, 2, 4, 4)
 
 #define MBS_LAUNCH_SIG const GemmArgs&, dim3, bool, bool, hipStream_t

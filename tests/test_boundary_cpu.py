@@ -200,3 +200,25 @@ def test_whole_k_tiles_refuse_k_tails_and_splits():
                                                256, 256, K, 256, snp, None, 0, None)
             assert st == 4, (names[c], K, splits)
             assert b"cannot run" in L.mbs_last_error()
+
+
+def test_grouped_whole_k_tiles_refuse_k_tails():
+    """The grouped launch's 32x32x64-MFMA configurations refuse K % 512 != 0
+    with MBS_ERR_CONFIG before any launch (the offsets are never read)."""
+    L = c_lib()
+    P, I = ctypes.c_void_p, ctypes.c_int
+    L.mbs_gemm_a4w4_grouped_launch_ex.argtypes = [P, P, P, P, P, P, P, I, P, I, I, I, I, I,
+                                                  ctypes.c_float, P, I, P]
+    L.mbs_gemm_a4w4_grouped_launch_ex.restype = I
+    L.mbs_gemm_a4w4_grouped_config_name.restype = ctypes.c_char_p
+    names = [L.mbs_gemm_a4w4_grouped_config_name(i).decode()
+             for i in range(L.mbs_gemm_a4w4_grouped_num_configs())]
+    m32 = [i for i, n in enumerate(names) if n.endswith("_m32")]
+    assert len(m32) == 2
+    for c in m32:
+        for K in (448, 1536 + 64, 1024 + 128):
+            snp = ((K // 32) + 7) // 8 * 8
+            st = L.mbs_gemm_a4w4_grouped_launch_ex(FAKE, FAKE, FAKE, FAKE, None, None, FAKE, 4, FAKE,
+                                                   256, 256, K, 256, snp, 1.0, None, c, None)
+            assert st == 4, (names[c], K)
+            assert b"cannot run" in L.mbs_last_error()

@@ -58,7 +58,7 @@ def dense_expert(dev, e, offs, N, K, xp, xs, wq, af, bf):
     return mbs_amd.gemm_a4w4(A, B, As, Bs, Af, Bf)
 
 
-@pytest.mark.parametrize("config", [0, 1, 2, 3])
+@pytest.mark.parametrize("config", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("rows,N,K", [([64, 0, 96, 32], 512, 1024), ([256, 128], 256, 2048)])
 def test_grouped_matches_dense_per_expert(dev, config, rows, N, K):
     import torch
@@ -113,7 +113,7 @@ def test_grouped_default_plan(dev, rows, N, K, factors):
         assert_close(bf16_to_f32(got[r0:r1]), ref, f"expert {e}")
 
 
-@pytest.mark.parametrize("config", [0, 1, 2, 3])
+@pytest.mark.parametrize("config", [0, 1, 2, 3, 4, 5])
 def test_grouped_alpha_bias(dev, config):
     """Affine epilogue per expert: bf16(C * alpha * f(a) * f(b) + bias[e]) --
     the dense launch of each expert with its own bias row, bit for bit, and
@@ -182,7 +182,7 @@ def _grouped_c_call(dev, A, B, As, Bs, goff, E, M, N, K, out, config=-1):
                                           stream_ptr())
 
 
-@pytest.mark.parametrize("config", [0, 1, 2, 3])
+@pytest.mark.parametrize("config", [0, 1, 2, 3, 4, 5])
 def test_grouped_all_experts_empty_writes_nothing(dev, config):
     """Every expert empty (offsets all 0) with M > 0: the kernel has no work
     units; every workgroup leaves before its first load and the output keeps
