@@ -159,6 +159,14 @@ struct BdShape {
     // A DMAs per stage: half a pair (BM/2 rows x 128 bytes, 8 rows each),
     // DA per wave.
     static constexpr int DA = (AF + NW - 1) / NW;
+    // ADEAL: AF is not a multiple of the wave count but 2 AF is (96 rows: 12
+    // DMAs per pair over 4 waves).  The pair's DMAs are then dealt DAP per
+    // wave (rows 8 DAP w .. of the slot), DAE of them on its even stage and
+    // DAO on the odd one, instead of DA per half with fillers.
+    static constexpr bool ADEAL = (AF % NW != 0) && ((2 * AF) % NW == 0);
+    static constexpr int DAP = ADEAL ? 2 * AF / NW : 2 * DA;
+    static constexpr int DAE = ADEAL ? (DAP + 1) / 2 : DA, DAO = ADEAL ? DAP / 2 : DA;
+    static constexpr int NVA = ADEAL ? DAP : DA;        // per-lane A DMA offsets kept
     // scale dwords read per wave per 256-K group: one per 32 rows / columns
     // (16x16x128), two per 32 rows / columns (32x32x64: combined by v_perm)
     static constexpr int SA = M32 ? FM : FM / 2, SB = M32 ? FN : FN / 2;
@@ -397,11 +405,12 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     // Per-lane offsets within a tile, fixed for the whole kernel.
     // A DMA j of a pair half: lane i -> row 8j + i/8 of the half, physical
     // chunk i%8, which holds global chunk (i%8) ^ swz(row); swz(row) = i/8
-    // since the half starts at a multiple of 8 rows.
+    // since the half starts at a multiple of 8 rows (ADEAL: j counts the
+    // DMAs of the whole pair, rows 8j + i/8 of the slot).
     // cA: the lane's K-byte offset in the pair (K-tail and dead-stage masks).
-    uint32_t voA[T::DA], cA[T::DA];
-    static_for<T::DA>([&](auto d) {
-        const int j = w * T::DA + d;
+    uint32_t voA[T::NVA], cA[T::NVA];
+    static_for<T::NVA>([&](auto d) {
+        const int j = w * (T::ADEAL ? T::DAP : T::DA) + d;
         const int c = (lane & 7) ^ (lane >> 3);
         cA[d] = (uint32_t)(c * 16);
         voA[d] = (uint32_t)((8 * j + (lane >> 3)) * Kp + c * 16);
@@ -547,17 +556,27 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     // pair's scalar offset (kOOB + small when dead); GEN kernels also mask
     // the lanes whose chunk lies past the pair's `vb` live bytes (K tail,
     // dead stage).  When AF is not a multiple of the wave count, the surplus
-    // DMAs read out of range into fjunk, so every wave issues DA of them.
+    // DMAs read out of range into fjunk, so every wave issues DA of them;
+    // ADEAL tiles issue DMA w*DAP + d (stage H = 0) or w*DAP + DAE + d (H = 1)
+    // of the whole pair instead.
     auto a_dma = [&](auto PK, auto H, auto D, uint32_t soff, int vb) __attribute__((always_inline)) {
         constexpr int d = decltype(D)::value, h = decltype(H)::value;
-        const int j = w * T::DA + d;
-        uint32_t vo = voA[d];
-        if constexpr (GEN) vo |= ((int)cA[d] >= vb) ? kOOB : 0u;
-        const uint32_t so = soff + (uint32_t)(h * (T::BM / 2) * Kp);
-        if (T::AF % T::NW == 0 || j < T::AF)
-            dma16s(rA, qp(PK) + h * (T::BM / 2) * 128 + j * 1024, vo, so);
-        else
-            dma16s(rA, fjunk, voA[d], kOOB);
+        if constexpr (T::ADEAL) {   // rows 8 jd .. of the slot, no fillers
+            constexpr int dd = (h ? T::DAE : 0) + d;
+            const int jd = w * T::DAP + dd;
+            uint32_t vo = voA[dd];
+            if constexpr (GEN) vo |= ((int)cA[dd] >= vb) ? kOOB : 0u;
+            dma16s(rA, qp(PK) + jd * 1024, vo, soff);
+        } else {
+            const int j = w * T::DA + d;
+            uint32_t vo = voA[d];
+            if constexpr (GEN) vo |= ((int)cA[d] >= vb) ? kOOB : 0u;
+            const uint32_t so = soff + (uint32_t)(h * (T::BM / 2) * Kp);
+            if (T::AF % T::NW == 0 || j < T::AF)
+                dma16s(rA, qp(PK) + h * (T::BM / 2) * 128 + j * 1024, vo, so);
+            else
+                dma16s(rA, fjunk, voA[d], kOOB);
+        }
     };
     // Scalar offset and live bytes of the A pair DMA'd at local stage ls
     // (the pair starting at stage (ls & ~1) + 4, possibly the next unit's).
@@ -583,20 +602,21 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         __attribute__((always_inline)) {
         constexpr int u = decltype(U)::value;
         constexpr int d = decltype(D)::value;
-        if constexpr (d < T::DA) {
+        constexpr int DAu = (u & 1) ? T::DAO : T::DAE;
+        if constexpr (d < DAu) {
             a_dma(std::integral_constant<int, (u >> 1) + 2>{}, std::integral_constant<int, u & 1>{},
                   std::integral_constant<int, d>{}, ta.a, ta.vb);
-        } else if constexpr (d < T::DA + T::FN) {
-            constexpr int j = d - T::DA;
+        } else if constexpr (d < DAu + T::FN) {
+            constexpr int j = d - DAu;
             rb[(u + 3) & 3][j] = load16s(rB, voB[j] | t3.tv, t3.b);
         } else {
             scale_dma(std::integral_constant<int, ((u + 3) >> 1) & 1>{},
-                      std::integral_constant<int, d - T::DA - T::FN>{}, t3);
+                      std::integral_constant<int, d - DAu - T::FN>{}, t3);
         }
     };
     // Issues per stage: NI_EVEN on even stages, NI_ODD on odd ones.
-    constexpr int NI_EVEN = T::DA + T::FN;
-    constexpr int NI_ODD = T::DA + T::FN + T::NSDW;
+    constexpr int NI_EVEN = T::DAE + T::FN;
+    constexpr int NI_ODD = T::DAO + T::FN + T::NSDW;
     // VMEM operations of an epilogue, all issued unconditionally: the bf16
     // stores (one per fragment pair and row block) and the factor DMAs of the
     // next unit (FD per wave).  vmcnt retires in issue order, so the first
@@ -935,7 +955,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     auto a_pair = [&](auto P) __attribute__((always_inline)) {
         const TgtA t = target_a(2 * decltype(P)::value - 4);
         static_for<2>([&](auto H) {
-            static_for<T::DA>([&](auto d) { a_dma(P, H, d, t.a, t.vb); });
+            static_for<decltype(H)::value ? T::DAO : T::DAE>([&](auto d) { a_dma(P, H, d, t.a, t.vb); });
         });
     };
     a_pair(std::integral_constant<int, 0>{});
@@ -946,7 +966,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     // The first stage is entered as if stages "-2" and "-1" had run: wait
     // for everything but A pair 1 and B stages 1 and 2, then read the scales
     // of group 0 and A fragments 0 and 1.
-    wait_vmcnt<2 * T::DA + 2 * T::FN>();
+    wait_vmcnt<T::DAE + T::DAO + 2 * T::FN>();
     barrier();
     static_for<NSR>([&](auto KI) {
         read_scale(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, KI);
