@@ -308,7 +308,7 @@ double plan_cost(const Plan& pl, int M, int N, int K)
 // factors (a sweep run in order is biased by the clock's response to
 // sustained load).  Entries naming an _m32 (32x32x64 MFMA) tile: medians of
 // 3 x 7 interleaved rounds against the 16x16x128 tiles, without / with
-// factors; the two 96x256 entries: means of 2 x 7 rounds, after the 96-row
+// factors; the three 96x256 entries: 2 x 7 (one: 7) rounds, after the 96-row
 // tiles' A DMAs were dealt without fillers (which made the 16x16x128 96x256
 // tile 7-11% faster; its stage cost above is scaled by that).
 struct TunedPlan {
@@ -317,7 +317,7 @@ struct TunedPlan {
     int splits;
 };
 const TunedPlan kTuned[] = {
-    {1024, 17408, 5120, "bdirect_128x384_w1x4_m32", 1},  // 50.41 / 53.84 us (128x384 1x4: 51.80 / 54.15)
+    {1024, 17408, 5120, "bdirect_96x256_w1x4", 1},  // 50.78 / 51.83 us (128x384 m32: 51.53 / 53.15; 96x256 m32: 52.57 / 53.37)
     {1024, 1024, 5120, "bdirect_64x128_w1x2", 1},  // 10.7 us
     {256, 7168, 2048, "bdirect_64x128_w1x2", 1},  // 7.1 us
     {2048, 7168, 2048, "bdirect_256x256_w1x4", 1},  // 22.04 / 23.85 us (2x2: 22.78 / 24.38; 256x256 1x4 m32: 22.03 / 23.95)
