@@ -217,6 +217,24 @@ struct Unit {
 // unswizzled 128-byte rows conflict 4-way, this pattern not at all).
 __device__ __forceinline__ int a_swz(int r) { return r & 7; }
 
+// Gap (after MFMA g of a stage's ng) at which VMEM item d of the stage's ni
+// issues: the items are spread over gaps [rw + rw/2, ng - rw/2).
+__host__ __device__ constexpr int item_gap(int d, int ni, int ng, int rw)
+{
+    const int span = ng - 2 * rw > 0 ? ng - 2 * rw : 1;
+    const int gi = rw + rw / 2 + d * span / ni;
+    return gi < ng ? gi : ng - 1;
+}
+// Items [first, ni) of a stage that issue in a later gap than item first-1.
+// Loads that share a gap may be issued in either order (only the gaps are
+// fenced), so only these are known to be issued after item first-1.
+__host__ __device__ constexpr int items_after_gap_of(int first, int ni, int ng, int rw)
+{
+    int n = 0;
+    for (int d = first; d < ni; ++d) n += item_gap(d, ni, ng, rw) > item_gap(first - 1, ni, ng, rw) ? 1 : 0;
+    return n;
+}
+
 // Persistent B-direct kernel: gridDim.x workgroups (at most one resident
 // set per CU) walk work units id = blockIdx.x + i*gridDim.x.  Per unit the
 // K loop runs n_st4 = round_up(sps, 4) stages (stages past the split end are
@@ -595,28 +613,32 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         t.a = t.vb > 0 ? o.a + (uint32_t)xl * 64u : kOOB;
         return t;
     };
-    // VMEM items issued at local stage ls (static slot u = ls & 3): DA
-    // A-DMAs and FN B-loads for stage ls+3 and, on odd stages, the NSDW scale
-    // DMAs of 256-K group (ls+3)/2 into buffer ((ls+3)/2) & 1.
+    // VMEM items issued at local stage ls (static slot u = ls & 3), in this
+    // order: DAE / DAO A-DMAs, on odd stages the NSDW scale DMAs of 256-K
+    // group (ls+3)/2 into buffer ((ls+3)/2) & 1, then the FN B-loads for
+    // stage ls+3 (last, so that odd stages can leave them in flight).
     auto issue_item = [&](auto U, auto D, const Tgt& t3, const TgtA& ta)
         __attribute__((always_inline)) {
         constexpr int u = decltype(U)::value;
         constexpr int d = decltype(D)::value;
         constexpr int DAu = (u & 1) ? T::DAO : T::DAE;
+        constexpr int NSu = (u & 1) ? T::NSDW : 0;
         if constexpr (d < DAu) {
             a_dma(std::integral_constant<int, (u >> 1) + 2>{}, std::integral_constant<int, u & 1>{},
                   std::integral_constant<int, d>{}, ta.a, ta.vb);
-        } else if constexpr (d < DAu + T::FN) {
-            constexpr int j = d - DAu;
-            rb[(u + 3) & 3][j] = load16s(rB, voB[j] | t3.tv, t3.b);
-        } else {
+        } else if constexpr (d < DAu + NSu) {
             scale_dma(std::integral_constant<int, ((u + 3) >> 1) & 1>{},
-                      std::integral_constant<int, d - DAu - T::FN>{}, t3);
+                      std::integral_constant<int, d - DAu>{}, t3);
+        } else {
+            constexpr int j = d - DAu - NSu;
+            rb[(u + 3) & 3][j] = load16s(rB, voB[j] | t3.tv, t3.b);
         }
     };
     // Issues per stage: NI_EVEN on even stages, NI_ODD on odd ones.
     constexpr int NI_EVEN = T::DAE + T::FN;
     constexpr int NI_ODD = T::DAO + T::FN + T::NSDW;
+    // B loads of an odd stage known to issue after its scale DMAs.
+    constexpr int NB_LATE = items_after_gap_of(T::DAO + T::NSDW, NI_ODD, T::FM * T::RW, T::RW);
     // VMEM operations of an epilogue, all issued unconditionally: the bf16
     // stores (one per fragment pair and row block) and the factor DMAs of the
     // next unit (FD per wave).  vmcnt retires in issue order, so the first
@@ -624,7 +646,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     // partial stores exceed the 6-bit count and are waited for).
     constexpr int FD = (T::NW == 1 ? 2 : 1) + T::FBB;   // factor + bias DMAs per wave
     constexpr int EPI_OPS = SPLIT ? 0 : T::FM * (T::FN / 2) + FD;
-    static_assert(NI_EVEN + EPI_OPS <= 63 && NI_ODD <= 63, "vmcnt is 6 bits");
+    static_assert(NI_EVEN + T::FN + EPI_OPS <= 63 && NI_EVEN + NI_ODD <= 63, "vmcnt is 6 bits");
 
     // A fragment x of the wave, half H of pair K of the iteration -> ra[R].
     // M32: fragment row x is 32-row block x % FM32 at 64-K step
@@ -672,7 +694,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     // at most a few other instructions, spread so that with one wave per
     // SIMD the matrix pipe is never starved by a burst of issues:
     //   gap FN*c      the look-ahead A read (fragment c+2, possibly of the next stage)
-    //   gap item_gap  the VMEM items (A DMAs, B loads, scale DMAs) of stage ls+3
+    //   gap item_gap  the VMEM items (A DMAs, scale DMAs on odd stages, B loads)
     //   gap scale_gap the next scale group's dwords (odd stages)
     // FIRST: the unit's first stage; its MFMAs start the accumulators from 0.
     // `post`: stage of the first iteration of a unit that follows an
@@ -685,26 +707,31 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         constexpr int NI = ((u & 1) == 0) ? NI_EVEN : NI_ODD;   // issues of this stage
         constexpr int NIP = ((u & 1) == 0) ? NI_ODD : NI_EVEN;  // issues of the previous one
         constexpr int NG = T::FM * RW;                          // MFMAs (= gaps) per stage
-        // Everything issued two or more stages ago has landed (A of ls+1 for
-        // this stage's look-ahead reads, B and scales of ls); the previous
-        // stage's issues may still be in flight.
+        // Stage-top wait.  Odd stages read the next scale group, DMA'd two
+        // stages ago: everything issued two or more stages ago has landed
+        // except that stage's B loads issued after its last scale DMA (B is
+        // issued last on odd stages, and B of stage ls+1 is not needed yet).
+        // Even stages need only their B (issued three stages ago) and A
+        // halves DMA'd three or more stages ago: the two previous stages'
+        // issues may still be in flight.
+        constexpr int WAITN = (u & 1) ? NIP + NB_LATE : NI_ODD + NI_EVEN;
         ph.mark((u == 0 && post) ? kPhNext : kPhBody);
         ph.stage();
         if constexpr (u == 0) {
             if (!post) {
-                wait_vmcnt<NIP>();
+                wait_vmcnt<WAITN>();
                 ph.mark(kPhWait);
                 barrier();
                 ph.mark(kPhBar);
             }
         } else if constexpr (u == 1) {
-            if (post) wait_vmcnt<NIP + EPI_OPS>();
-            else wait_vmcnt<NIP>();
+            if (post) wait_vmcnt<WAITN + EPI_OPS>();
+            else wait_vmcnt<WAITN>();
             ph.mark(kPhWait);
             barrier();
             ph.mark(kPhBar);
         } else {
-            wait_vmcnt<NIP>();
+            wait_vmcnt<WAITN>();
             ph.mark(kPhWait);
             barrier();
             ph.mark(kPhBar);
@@ -814,10 +841,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             }
             // VMEM items over gaps [RW + RW/2, NG - RW/2)
             static_for<NI>([&](auto D) {
-                constexpr int d = decltype(D)::value;
-                constexpr int span = NG - 2 * RW > 0 ? NG - 2 * RW : 1;
-                constexpr int gi = RW + RW / 2 + d * span / NI;
-                if constexpr ((gi < NG ? gi : NG - 1) == g) issue_item(U, D, t3, ta);
+                if constexpr (item_gap(decltype(D)::value, NI, NG, RW) == g) issue_item(U, D, t3, ta);
             });
             // Odd stages: the next group's scale dwords (DMA'd two stages
             // ago), after this gap's fragment read.
@@ -1040,7 +1064,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         // also makes this unit's factor bytes (and the table) visible.
         ph.mark(kPhBody);
         ph.unit();
-        wait_vmcnt<NI_ODD>();
+        wait_vmcnt<NI_ODD + NI_EVEN>();
         ph.mark(kPhWait);
         barrier();
         ph.mark(kPhBar);
