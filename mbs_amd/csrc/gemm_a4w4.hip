@@ -158,7 +158,7 @@ const Config kConfigs[] = {
     {"bdirect_256x128_w1x4", kPersistent, 256, 128, 256, 1, {0.383f, 0.383f, 3.03f}, launch_bdirect<B256x128w14>, true},
     {"bdirect_128x256_w1x4", kPersistent, 128, 256, 256, 1, {0.367f, 0.367f, 3.14f}, launch_bdirect<B128x256w14>, true},
     {"bdirect_192x256_w1x4", kPersistent, 192, 256, 256, 1, {0.467f, 0.467f, 4.17f}, launch_bdirect<B192x256w14>, true},
-    {"bdirect_96x256_w1x4", kPersistent, 96, 256, 256, 1, {0.308f, 0.308f, 2.77f}, launch_bdirect<B96x256w14>, true},
+    {"bdirect_96x256_w1x4", kPersistent, 96, 256, 256, 1, {0.290f, 0.290f, 2.77f}, launch_bdirect<B96x256w14>, true},
     {"bdirect_64x512_w1x4", kPersistent, 64, 512, 256, 1, {0.428f, 0.428f, 3.26f}, launch_bdirect<B64x512w14>, true},
     {"bdirect_128x384_w1x4", kPersistent, 128, 384, 256, 1, {0.455f, 0.455f, 4.55f}, launch_bdirect<B128x384w14>, true},
     // v_mfma_scale_f32_32x32x64_f8f6f4 tiles
@@ -308,27 +308,28 @@ double plan_cost(const Plan& pl, int M, int N, int K)
 // factors (a sweep run in order is biased by the clock's response to
 // sustained load).  Entries naming an _m32 (32x32x64 MFMA) tile: medians of
 // 3 x 7 interleaved rounds against the 16x16x128 tiles, without / with
-// factors; the three 96x256 entries: 2 x 7 (one: 7) rounds, after the 96-row
-// tiles' A DMAs were dealt without fillers (which made the 16x16x128 96x256
-// tile 7-11% faster; its stage cost above is scaled by that).
+// factors.  The five mid-M entries at K >= 5120 were re-measured (2 x 7
+// rounds) after the 96-row tiles' A DMAs were dealt without fillers and the
+// stage-top waits relaxed, which made the 96-row tiles 11-19% faster in
+// all (their stage cost above is scaled by 0.87).
 struct TunedPlan {
     int M, N, K;
     const char* config;
     int splits;
 };
 const TunedPlan kTuned[] = {
-    {1024, 17408, 5120, "bdirect_96x256_w1x4", 1},  // 50.78 / 51.83 us (128x384 m32: 51.53 / 53.15; 96x256 m32: 52.57 / 53.37)
+    {1024, 17408, 5120, "bdirect_96x256_w1x4", 1},  // 51.48 / 55.27 us (96x256 m32: 53.20 / 57.22; 128x384 m32: 54.38 / 58.51)
     {1024, 1024, 5120, "bdirect_64x128_w1x2", 1},  // 10.7 us
     {256, 7168, 2048, "bdirect_64x128_w1x2", 1},  // 7.1 us
     {2048, 7168, 2048, "bdirect_256x256_w1x4", 1},  // 22.04 / 23.85 us (2x2: 22.78 / 24.38; 256x256 1x4 m32: 22.03 / 23.95)
     {256, 4096, 7168, "bdirect_64x128_w1x2", 1},  // 13.1 us
-    {2048, 4096, 7168, "bdirect_128x256_w1x4_m32", 1},  // 33.38 / 34.62 us (128x256 1x4: 34.40 / 34.94)
+    {2048, 4096, 7168, "bdirect_128x256_w1x4_m32", 1},  // 34.42 / 35.95 us (128x256 1x4: 34.40 / 34.94 before; 96x256: 42.51 / 44.62)
     {256, 2112, 7168, "bdirect_64x128_w1x2", 2},  // 13.1 us
-    {2048, 2112, 7168, "bdirect_96x256_w1x4_m32", 1},  // 25.48 / 26.38 us (128x256 m32: 25.81 / 27.15; 96x256: 25.48 / 26.54)
+    {2048, 2112, 7168, "bdirect_96x256_w1x4_m32", 1},  // 24.24 / 25.09 us (96x256: 25.71 / 26.58; 128x256 m32: 25.81 / 27.15 before)
     {1000, 1280, 512, "bdirect_64x128_w1x2", 1},  // 4.9 us
     {3333, 5120, 512, "bdirect_64x128_w1x2", 1},  // 15.3 us
-    {1000, 5120, 12288, "bdirect_128x256_w1x4_m32", 1},  // 40.01 / 40.32 us (128x256 1x4: 41.74 / 42.37)
-    {3333, 1280, 12288, "bdirect_96x256_w1x4_m32", 1},  // 36.46 / 37.94 us (96x256: 36.84 / 38.19; 128x256 m32: 39.16 / 40.76)
+    {1000, 5120, 12288, "bdirect_96x256_w1x4", 1},  // 39.21 / 40.25 us (96x256 m32: 40.85 / 41.23; 128x256 m32: 42.22 / 42.28)
+    {3333, 1280, 12288, "bdirect_96x256_w1x4_m32", 1},  // 34.72 / 36.10 us (96x256: 36.67 / 37.24; 128x256 m32: 39.16 / 40.76 before)
     {8192, 10240, 5120, "bdirect_256x256_w2x2", 1},  // 186.5 us
     {8192, 17408, 5120, "bdirect_192x256_w1x4", 1},  // 327.5 us
     {8192, 5120, 17408, "bdirect_256x256_w2x2", 1},  // 295.7 us
