@@ -189,7 +189,12 @@ struct BdShape {
     static_assert(BM <= 256, "one 256-byte chunk of A factor bytes");
     static_assert(NW == 1 ? NBC == 1 : NW >= 1 + NBC, "one factor DMA per wave");
     static_assert(BM % 16 == 0, "pair halves of whole 8-row DMA groups");
-    static_assert(3 * PSLOT + 2 * SBUF <= 150 * 1024, "LDS budget");
+    // A pair slots: four where they fit (96-192 rows, 256+ columns), three
+    // otherwise.  With four, a slot's previous pair was last read three
+    // stages before the DMA that rewrites it (the barrier of the odd stage
+    // in between covers it), so even stages wait without a barrier.
+    static constexpr int NSLOT = (BM >= 96 && BM <= 192 && BN >= 256) ? 4 : 3;
+    static_assert(NSLOT * PSLOT + 2 * SBUF <= 150 * 1024, "LDS budget");
     // Epilogue stores staged through LDS (whole rows per neighbouring lanes)
     // for tiles of 96+ rows; the 64-row tiles, whose short epilogues run with
     // 2-4 workgroups per CU, store straight from registers (the staged form
@@ -248,10 +253,11 @@ __host__ __device__ constexpr int items_after_gap_of(int first, int ni, int ng, 
 // ls+3 and (odd ls) scale group (ls+3)/2; the A DMA of half (ls & 1) of the
 // pair starting at stage (ls & ~1) + 4.  A pair slot is rewritten only after
 // the barrier that follows the last read of its previous pair, and the
-// stage-top wait (everything issued two or more stages ago has landed)
-// covers every pair before its first read, with three slots.  The slot of a
-// pair is its running index mod 3 across units: the three slot pointers
-// rotate by one position per 4-stage iteration (two pairs).  A fragment and
+// stage-top waits cover every pair before its first read, with three slots.
+// The slot of a pair is its running index mod 3 across units: the three slot
+// pointers rotate by one position per 4-stage iteration (two pairs).  Tiles
+// with four slots (BdShape::NSLOT) swap them pairwise instead, and their even
+// stages need no barrier.  A fragment and
 // scale reads are explicit ds_read instructions with counted lgkmcnt waits
 // (the compiler would otherwise make them wait for the A DMA into the
 // dynamically chosen slot).
@@ -275,6 +281,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     __shared__ __attribute__((aligned(1024))) uint8_t pa0[T::PSLOT];
     __shared__ __attribute__((aligned(1024))) uint8_t pa1[T::PSLOT];
     __shared__ __attribute__((aligned(1024))) uint8_t pa2[T::PSLOT];
+    __shared__ __attribute__((aligned(T::NSLOT == 4 ? 1024 : 4))) uint8_t pa3[T::NSLOT == 4 ? T::PSLOT : 4];
     // MBS factor bytes of a unit (A rows at [0,256), B columns at [256,512)),
     // double-buffered by unit parity, and the byte -> fp32 factor table.
     __shared__ __attribute__((aligned(16))) uint8_t fbytes[2][T::FBW];
@@ -294,12 +301,16 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     // Pair slots of the current 4-stage iteration: q0 (pair 0, stages 0-1),
     // q1 (pair 1, stages 2-3), q2 (pair 2, DMA'd by stages 0-1); pair 3 (DMA'd
     // by stages 2-3) reuses q0.  Next iteration: (q0, q1, q2) <- (q2, q0, q1).
+    // Four slots: pair 3 goes to q3, and (q0, q1, q2, q3) <- (q2, q3, q0, q1).
     uint8_t* q0 = pa0;
     uint8_t* q1 = pa1;
     uint8_t* q2 = pa2;
+    uint8_t* q3 = nullptr;
+    if constexpr (T::NSLOT == 4) q3 = pa3;
     auto qp = [&](auto K) __attribute__((always_inline)) -> uint8_t* {
         constexpr int k = decltype(K)::value & 3;
-        if constexpr (k == 0 || k == 3) return q0;
+        if constexpr (k == 3 && T::NSLOT == 4) return q3;
+        else if constexpr (k == 0 || k == 3) return q0;
         else if constexpr (k == 1) return q1;
         else return q2;
     };
@@ -715,13 +726,17 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         // halves DMA'd three or more stages ago: the two previous stages'
         // issues may still be in flight.
         constexpr int WAITN = (u & 1) ? NIP + NB_LATE : NI_ODD + NI_EVEN;
+        // Four slots: the even stages' data (three stages old) was published
+        // by the previous odd stage's barrier, and their DMAs rewrite a slot
+        // last read before it: a per-wave wait (for B) suffices.
+        constexpr bool BAR = (u & 1) || T::NSLOT == 3;
         ph.mark((u == 0 && post) ? kPhNext : kPhBody);
         ph.stage();
         if constexpr (u == 0) {
             if (!post) {
                 wait_vmcnt<WAITN>();
                 ph.mark(kPhWait);
-                barrier();
+                if constexpr (BAR) barrier();
                 ph.mark(kPhBar);
             }
         } else if constexpr (u == 1) {
@@ -733,7 +748,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
         } else {
             wait_vmcnt<WAITN>();
             ph.mark(kPhWait);
-            barrier();
+            if constexpr (BAR) barrier();
             ph.mark(kPhBar);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1030,6 +1045,15 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     using FT = std::integral_constant<bool, true>;
     using FF = std::integral_constant<bool, false>;
     auto rotate = [&]() __attribute__((always_inline)) {
+        if constexpr (T::NSLOT == 4) {
+            uint8_t* t = q0;
+            q0 = q2;
+            q2 = t;
+            t = q1;
+            q1 = q3;
+            q3 = t;
+            return;
+        }
         uint8_t* t = q2;
         q2 = q1;
         q1 = q0;
@@ -1047,10 +1071,12 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             stage(I0{}, FT{}, 0, post);
             stage(I1{}, FF{}, 1, post);
             stage(I2{}, FF{}, 2, false);
-            // the wait of stage 2 covers the factor DMAs issued with the
-            // previous epilogue (stage 1's may leave them in flight)
-            convert_factors(par, cur.m0);
+            // the wait and barrier of stage 2 (four slots: 3) cover the
+            // factor DMAs issued with the previous epilogue (stage 1's may
+            // leave them in flight)
+            if constexpr (T::NSLOT == 3) convert_factors(par, cur.m0);
             stage(I3{}, FF{}, 3, false);
+            if constexpr (T::NSLOT == 4) convert_factors(par, cur.m0);
             rotate();
         }
         for (int ls0 = 4; ls0 < n_st4; ls0 += 4) {
