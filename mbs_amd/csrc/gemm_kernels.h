@@ -122,6 +122,11 @@ inline bool affine_epilogue(const GemmArgs& a)
 {
     return (a.Af != nullptr && a.Bf != nullptr) || a.bias != nullptr || a.alpha != 1.0f;
 }
+// Epilogue form of a launch: 0 plain, 1 factors / alpha, 2 also a bias.
+inline int epilogue_form(const GemmArgs& a)
+{
+    return a.bias != nullptr ? 2 : affine_epilogue(a) ? 1 : 0;
+}
 
 // ======================================================================
 // B-direct persistent kernel
@@ -267,16 +272,18 @@ __host__ __device__ constexpr int items_after_gap_of(int first, int ni, int ng, 
 // factors are offset to expert e, and rows past the expert's end, which
 // belong to the next expert, are computed but not stored.
 //
-// AFF: the bf16 epilogue applies MBS factors, alpha and the column bias.  It
-// is a separate instantiation so that the plain epilogue's register
-// allocation is not sized for the scaled one's extra live values (which
-// would spill into scratch, and each scratch reload waits on the next
-// unit's outstanding DMAs).
-template <class T, bool GEN, bool SPLIT, bool GROUPED = false, bool AFF = false>
+// AFF: the bf16 epilogue applies MBS factors and alpha (1), and the column
+// bias (2).  Each form is a separate instantiation so that the plain
+// epilogue's register allocation is not sized for the scaled one's extra
+// live values (which would spill into scratch, and each scratch reload
+// waits on the next unit's outstanding DMAs); the form without a bias saves
+// a third of the scaled epilogue's per-element arithmetic.
+template <class T, bool GEN, bool SPLIT, bool GROUPED = false, int AFF = 0>
 __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
 {
     static_assert(!(GROUPED && SPLIT), "grouped GEMM runs without K splits");
     static_assert(!(AFF && SPLIT), "split launches write fp32 partial sums");
+    static_assert(AFF >= 0 && AFF <= 2, "epilogue form");
     static_assert(!T::M32 || (!GEN && !SPLIT), "M32 tiles: whole-K, single-split");
     __shared__ __attribute__((aligned(1024))) uint8_t pa0[T::PSLOT];
     __shared__ __attribute__((aligned(1024))) uint8_t pa1[T::PSLOT];
@@ -1125,8 +1132,9 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             // (each form is defined only where it is used: their accumulator
             // expressions do not depend on the lambdas' own parameters)
             if constexpr (!T::M32) {
-            auto epi = [&](auto HF) __attribute__((always_inline)) {
+            auto epi = [&](auto HF, auto BZ) __attribute__((always_inline)) {
                 constexpr bool hf = decltype(HF)::value;
+                constexpr bool bz = hf && decltype(BZ)::value;   // a bias to add
                 float fa[T::FM];
                 if constexpr (hf) {
                     static_for<T::FM>([&](auto i) { fa[i] = frowf[par][row_l + i * 16]; });
@@ -1150,6 +1158,9 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                             e.f0[k] = c0[k];
                             e.f1[k] = c1[k];
                         });
+                    }
+                    if constexpr (bz) {
+                        const int cl = wn * T::WN + j0 * 16 + q * 4;
                         const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&fbias[par][cl]);
                         const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&fbias[par][cl + 16]);
                         const uint32_t u0 = w0[0], u1 = w0[1], u2 = w1[0], u3 = w1[1];
@@ -1164,11 +1175,17 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                     __attribute__((always_inline)) {
                     constexpr int i = decltype(I)::value, j0 = decltype(J0)::value;
                     f32x4 v0 = acc[i][j0], v1 = acc[i][j0 + 1];
-                    if constexpr (hf) {
+                    if constexpr (bz) {
                         static_for<4>([&](auto K4) {
                             constexpr int k = decltype(K4)::value;
                             v0[k] = add_nc(v0[k] * (fa[i] * e.f0[k]), e.z0[k]);
                             v1[k] = add_nc(v1[k] * (fa[i] * e.f1[k]), e.z1[k]);
+                        });
+                    } else if constexpr (hf) {
+                        static_for<4>([&](auto K4) {
+                            constexpr int k = decltype(K4)::value;
+                            v0[k] = v0[k] * (fa[i] * e.f0[k]);
+                            v1[k] = v1[k] * (fa[i] * e.f1[k]);
                         });
                     }
                     uint32_t x0 = pack_bf16x2(v0[0], v0[1]), x1 = pack_bf16x2(v0[2], v0[3]);
@@ -1273,7 +1290,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                     });
                 }
             };
-            epi(std::integral_constant<bool, AFF>{});
+            epi(std::integral_constant<bool, AFF != 0>{}, std::integral_constant<bool, AFF == 2>{});
             } else {
             // M32: acc[c32][j] of lane L holds row c32*32 + L%32 of the wave
             // tile, columns 32j + 8q + 4v + i (q = r/4, i = r%4, v = L/32).
@@ -1285,24 +1302,27 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
             // stores per 32 rows.  A trailing single block (96-column wave
             // tiles) is staged as 32 x 64 bytes and stored with 4 lanes per
             // row: 2 stores.  Together FM * (FN / 2) stores (EPI_OPS).
-            auto epi32 = [&](auto HF) __attribute__((always_inline)) {
+            auto epi32 = [&](auto HF, auto BZ) __attribute__((always_inline)) {
                 constexpr bool hf = decltype(HF)::value;
+                constexpr bool bz = hf && decltype(BZ)::value;   // a bias to add
                 constexpr int NL = T::FN32 / 2;   // whole 128-byte lines
                 const int m = lane & 31, v = lane >> 5;
                 uint8_t* const stg = estage[w];
                 // the lane's column factors and bias words, read once for all
                 // row blocks: columns 32j + 8q + 4v .. +3
                 f32x4 fcol[hf ? T::FN32 : 1][hf ? 4 : 1];
-                uint32_t zw[hf ? T::FN32 : 1][hf ? 4 : 1][2];
+                uint32_t zw[bz ? T::FN32 : 1][bz ? 4 : 1][2];
                 if constexpr (hf) {
                     static_for<T::FN32>([&](auto J) {
                         static_for<4>([&](auto Q) {
                             constexpr int j = decltype(J)::value, q = decltype(Q)::value;
                             const int cl = wn * T::WN + 32 * j + 8 * q + 4 * v;
                             fcol[j][q] = *reinterpret_cast<const f32x4*>(&fcolf[par][cl]);
-                            const uint32_t* bw = reinterpret_cast<const uint32_t*>(&fbias[par][cl]);
-                            zw[j][q][0] = bw[0];
-                            zw[j][q][1] = bw[1];
+                            if constexpr (bz) {
+                                const uint32_t* bw = reinterpret_cast<const uint32_t*>(&fbias[par][cl]);
+                                zw[j][q][0] = bw[0];
+                                zw[j][q][1] = bw[1];
+                            }
                         });
                     });
                 }
@@ -1316,13 +1336,19 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                         constexpr int q = decltype(Q)::value;
                         float e[4];
                         static_for<4>([&](auto I) { e[decltype(I)::value] = acc[c32][j][4 * q + decltype(I)::value]; });
-                        if constexpr (hf) {
+                        if constexpr (bz) {
                             const f32x4 f = fcol[j][q];
                             const uint32_t b0 = zw[j][q][0], b1 = zw[j][q][1];
                             const float z[4] = {bf16_lo(b0), bf16_hi(b0), bf16_lo(b1), bf16_hi(b1)};
                             static_for<4>([&](auto I) {
                                 constexpr int i = decltype(I)::value;
                                 e[i] = add_nc(e[i] * (fa * f[i]), z[i]);
+                            });
+                        } else if constexpr (hf) {
+                            const f32x4 f = fcol[j][q];
+                            static_for<4>([&](auto I) {
+                                constexpr int i = decltype(I)::value;
+                                e[i] = e[i] * (fa * f[i]);
                             });
                         }
                         x[q][0] = pack_bf16x2(e[0], e[1]);
@@ -1382,7 +1408,7 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                     __builtin_amdgcn_sched_barrier(0);
                 });
             };
-            epi32(std::integral_constant<bool, AFF>{});
+            epi32(std::integral_constant<bool, AFF != 0>{}, std::integral_constant<bool, AFF == 2>{});
             }
         }
         ph.mark(kPhEpi);
@@ -1545,23 +1571,31 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
     }
 }
 
+// A non-split launch of the persistent kernel in the epilogue form the
+// arguments ask for.
+template <class T, bool GEN, bool GROUPED>
+void launch_bdirect_form(const GemmArgs& a, dim3 grid, hipStream_t s)
+{
+    switch (epilogue_form(a)) {
+    case 2: hipLaunchKernelGGL((gemm_bdirect_kernel<T, GEN, false, GROUPED, 2>), grid, dim3(T::NT), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((gemm_bdirect_kernel<T, GEN, false, GROUPED, 1>), grid, dim3(T::NT), 0, s, a); break;
+    default: hipLaunchKernelGGL((gemm_bdirect_kernel<T, GEN, false, GROUPED, 0>), grid, dim3(T::NT), 0, s, a);
+    }
+}
+
 template <class T>
 hipError_t launch_bdirect(const GemmArgs& a, dim3 grid, bool gen, bool split, hipStream_t s)
 {
-    const bool aff = affine_epilogue(a);
     if constexpr (T::M32) {
         // whole-K, single-split plans only (make_plan offers no other)
         if (gen || split) return hipErrorInvalidValue;
-        if (aff) hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false, false, true>), grid, dim3(T::NT), 0, s, a);
-        else hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false>), grid, dim3(T::NT), 0, s, a);
+        launch_bdirect_form<T, false, false>(a, grid, s);
     } else if (gen) {
         if (split) hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, true>), grid, dim3(T::NT), 0, s, a);
-        else if (aff) hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false, false, true>), grid, dim3(T::NT), 0, s, a);
-        else hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false>), grid, dim3(T::NT), 0, s, a);
+        else launch_bdirect_form<T, true, false>(a, grid, s);
     } else {
         if (split) hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, true>), grid, dim3(T::NT), 0, s, a);
-        else if (aff) hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false, false, true>), grid, dim3(T::NT), 0, s, a);
-        else hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false>), grid, dim3(T::NT), 0, s, a);
+        else launch_bdirect_form<T, false, false>(a, grid, s);
     }
     return hipGetLastError();
 }
@@ -1570,18 +1604,14 @@ hipError_t launch_bdirect(const GemmArgs& a, dim3 grid, bool gen, bool split, hi
 template <class T>
 hipError_t launch_bdirect_grouped(const GemmArgs& a, dim3 grid, bool gen, bool, hipStream_t s)
 {
-    const bool aff = affine_epilogue(a);
     if constexpr (T::M32) {
         // whole-K plans only (run_grouped refuses K % 512 != 0)
         if (gen) return hipErrorInvalidValue;
-        if (aff) hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false, true, true>), grid, dim3(T::NT), 0, s, a);
-        else hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false, true>), grid, dim3(T::NT), 0, s, a);
+        launch_bdirect_form<T, false, true>(a, grid, s);
     } else if (gen) {
-        if (aff) hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false, true, true>), grid, dim3(T::NT), 0, s, a);
-        else hipLaunchKernelGGL((gemm_bdirect_kernel<T, true, false, true>), grid, dim3(T::NT), 0, s, a);
+        launch_bdirect_form<T, true, true>(a, grid, s);
     } else {
-        if (aff) hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false, true, true>), grid, dim3(T::NT), 0, s, a);
-        else hipLaunchKernelGGL((gemm_bdirect_kernel<T, false, false, true>), grid, dim3(T::NT), 0, s, a);
+        launch_bdirect_form<T, false, true>(a, grid, s);
     }
     return hipGetLastError();
 }
