@@ -1251,15 +1251,21 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                     const uint8_t* const r0 = stg + r * 128 + ((cc ^ r) * 16);
                     const int col = col_w + j0 * 16 + cc * 8;   // N % 16 == 0
                     const bool store_ok = col < p.N;
+                    // Software-pipelined by one block: block i+1 is converted
+                    // while block i's staging round trip is in flight.
+                    uint32_t u[4], v[4];
+                    pair_bits(I0{}, std::integral_constant<int, j0>{}, e0, u);
+                    pair_bits(I0{}, std::integral_constant<int, j0 + 2>{}, e1, v);
                     static_for<T::FM>([&](auto I) {
                         constexpr int i = decltype(I)::value;
-                        uint32_t u[4], v[4];
-                        pair_bits(I, std::integral_constant<int, j0>{}, e0, u);
-                        pair_bits(I, std::integral_constant<int, j0 + 2>{}, e1, v);
                         *reinterpret_cast<f32x4*>(w0) = vec_of(u);
                         *reinterpret_cast<f32x4*>(w1) = vec_of(v);
                         const f32x4 x0 = *reinterpret_cast<const f32x4*>(r0);
                         const f32x4 x1 = *reinterpret_cast<const f32x4*>(r0 + 1024);
+                        if constexpr (i + 1 < T::FM) {
+                            pair_bits(std::integral_constant<int, i + 1>{}, std::integral_constant<int, j0>{}, e0, u);
+                            pair_bits(std::integral_constant<int, i + 1>{}, std::integral_constant<int, j0 + 2>{}, e1, v);
+                        }
                         const uint32_t o = (uint32_t)(((wm * T::WM + i * 16 + r) * p.N + col) * 2);
                         store16(rO, store_ok ? o : kOOB, x0);
                         store16(rO, store_ok ? o + (uint32_t)(8 * p.N * 2) : kOOB, x1);
@@ -1362,47 +1368,79 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
                         piece[decltype(H2)::value] = i32x4{(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]};
                     });
                 };
-                static_for<T::FM32>([&](auto C32) {
-                    constexpr int c32 = decltype(C32)::value;
+                // Jobs: per 32-row block c32, NL whole 128-byte lines and (odd
+                // FN32) the trailing 64-byte block.  Software-pipelined by one
+                // job: job k+1 is converted while job k's staging round trip
+                // is in flight.
+                constexpr int JPB = NL + (T::FN32 % 2);   // jobs per row block
+                constexpr int NJ = T::FM32 * JPB;
+                auto job_bits = [&](auto KJ, i32x4 (&pc)[4]) __attribute__((always_inline)) {
+                    constexpr int kj = decltype(KJ)::value;
+                    constexpr int c32 = kj / JPB, ln = kj % JPB;
                     float fa = 1.0f;
                     if constexpr (hf) fa = frowf[par][c32 * 32 + m];
-                    static_for<NL>([&](auto Ln) {
-                        constexpr int ln = decltype(Ln)::value;
+                    i32x4 a[2], b[2];
+                    if constexpr (ln < NL) {
+                        block_bits(std::integral_constant<int, c32>{}, std::integral_constant<int, 2 * ln>{}, fa, a);
+                        block_bits(std::integral_constant<int, c32>{}, std::integral_constant<int, 2 * ln + 1>{}, fa, b);
+                        pc[2] = b[0];
+                        pc[3] = b[1];
+                    } else {
+                        block_bits(std::integral_constant<int, c32>{}, std::integral_constant<int, T::FN32 - 1>{}, fa, a);
+                    }
+                    pc[0] = a[0];
+                    pc[1] = a[1];
+                };
+                i32x4 pc[4];
+                job_bits(std::integral_constant<int, 0>{}, pc);
+                static_for<NJ>([&](auto KJ) {
+                    constexpr int kj = decltype(KJ)::value;
+                    constexpr int c32 = kj / JPB, ln = kj % JPB;
+                    f32x4 xv[4];
+                    int col;
+                    if constexpr (ln < NL) {
+                        // pieces: chunk 4jj + 2h + v of the line
                         static_for<2>([&](auto J2) {
-                            constexpr int jj = decltype(J2)::value;
-                            i32x4 piece[2];
-                            block_bits(C32, std::integral_constant<int, 2 * ln + jj>{}, fa, piece);
                             static_for<2>([&](auto H2) {
-                                const int chunk = 4 * jj + 2 * decltype(H2)::value + v;
-                                *reinterpret_cast<i32x4*>(stg + m * 128 + ((chunk ^ (m & 7)) * 16)) =
-                                    piece[decltype(H2)::value];
+                                constexpr int jj = decltype(J2)::value, h2 = decltype(H2)::value;
+                                const int chunk = 4 * jj + 2 * h2 + v;
+                                *reinterpret_cast<i32x4*>(stg + m * 128 + ((chunk ^ (m & 7)) * 16)) = pc[2 * jj + h2];
                             });
                         });
                         const int rr = lane >> 3, cc = lane & 7;
-                        const int col = col_w + ln * 64 + cc * 8;   // N % 16 == 0
+                        col = col_w + ln * 64 + cc * 8;   // N % 16 == 0
                         static_for<4>([&](auto Bk) {
                             const int r = rr + 8 * decltype(Bk)::value;
-                            const f32x4 xv = *reinterpret_cast<const f32x4*>(stg + r * 128 + ((cc ^ (r & 7)) * 16));
-                            const uint32_t o = (uint32_t)(((c32 * 32 + r) * p.N + col) * 2);
-                            store16(rO, col < p.N ? o : kOOB, xv);
+                            xv[decltype(Bk)::value] = *reinterpret_cast<const f32x4*>(stg + r * 128 + ((cc ^ (r & 7)) * 16));
                         });
-                    });
-                    if constexpr (T::FN32 % 2 == 1) {
-                        i32x4 piece[2];
-                        block_bits(C32, std::integral_constant<int, T::FN32 - 1>{}, fa, piece);
+                    } else {
                         static_for<2>([&](auto H2) {
                             const int chunk = 2 * decltype(H2)::value + v;
                             *reinterpret_cast<i32x4*>(stg + m * 64 + ((chunk ^ ((m >> 1) & 3)) * 16)) =
-                                piece[decltype(H2)::value];
+                                pc[decltype(H2)::value];
                         });
                         const int rr = lane >> 2, cc = lane & 3;
-                        const int col = col_w + NL * 64 + cc * 8;
+                        col = col_w + NL * 64 + cc * 8;
                         static_for<2>([&](auto Bk) {
                             const int r = rr + 16 * decltype(Bk)::value;
-                            const f32x4 xv =
+                            xv[decltype(Bk)::value] =
                                 *reinterpret_cast<const f32x4*>(stg + r * 64 + ((cc ^ ((r >> 1) & 3)) * 16));
+                        });
+                    }
+                    if constexpr (kj + 1 < NJ) job_bits(std::integral_constant<int, kj + 1>{}, pc);
+                    if constexpr (ln < NL) {
+                        const int rr = lane >> 3;
+                        static_for<4>([&](auto Bk) {
+                            const int r = rr + 8 * decltype(Bk)::value;
                             const uint32_t o = (uint32_t)(((c32 * 32 + r) * p.N + col) * 2);
-                            store16(rO, col < p.N ? o : kOOB, xv);
+                            store16(rO, col < p.N ? o : kOOB, xv[decltype(Bk)::value]);
+                        });
+                    } else {
+                        const int rr = lane >> 2;
+                        static_for<2>([&](auto Bk) {
+                            const int r = rr + 16 * decltype(Bk)::value;
+                            const uint32_t o = (uint32_t)(((c32 * 32 + r) * p.N + col) * 2);
+                            store16(rO, col < p.N ? o : kOOB, xv[decltype(Bk)::value]);
                         });
                     }
                     __builtin_amdgcn_sched_barrier(0);
