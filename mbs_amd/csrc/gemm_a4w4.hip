@@ -311,7 +311,8 @@ double plan_cost(const Plan& pl, int M, int N, int K)
 // factors.  The five mid-M entries at K >= 5120 were re-measured (2 x 7
 // rounds) after the 96-row tiles' A DMAs were dealt without fillers and the
 // stage-top waits relaxed, which made the 96-row tiles 11-19% faster in
-// all (their stage cost above is scaled by 0.87).
+// all (their stage cost above is scaled by 0.87); six entries again after
+// the pipelined epilogue (2 x 7 rounds; "before": not re-measured).
 struct TunedPlan {
     int M, N, K;
     const char* config;
@@ -321,19 +322,19 @@ const TunedPlan kTuned[] = {
     {1024, 17408, 5120, "bdirect_96x256_w1x4", 1},  // 51.48 / 55.27 us (96x256 m32: 53.20 / 57.22; 128x384 m32: 54.38 / 58.51)
     {1024, 1024, 5120, "bdirect_64x128_w1x2", 1},  // 10.7 us
     {256, 7168, 2048, "bdirect_64x128_w1x2", 1},  // 7.1 us
-    {2048, 7168, 2048, "bdirect_256x256_w1x4", 1},  // 22.04 / 23.85 us (2x2: 22.78 / 24.38; 256x256 1x4 m32: 22.03 / 23.95)
+    {2048, 7168, 2048, "bdirect_256x256_w1x4", 1},  // 21.12 / 21.99 us (2x2: 21.59 / 22.76; 256x256 m32: 21.64 / 22.81)
     {256, 4096, 7168, "bdirect_64x128_w1x2", 1},  // 13.1 us
-    {2048, 4096, 7168, "bdirect_128x256_w1x4_m32", 1},  // 34.42 / 35.95 us (128x256 1x4: 34.40 / 34.94 before; 96x256: 42.51 / 44.62)
+    {2048, 4096, 7168, "bdirect_128x256_w1x4_m32", 1},  // 32.17 / 33.43 us (128x256 1x4: 33.06 / 33.61; 96x256: 42.51 / 44.62 before)
     {256, 2112, 7168, "bdirect_64x128_w1x2", 2},  // 13.1 us
-    {2048, 2112, 7168, "bdirect_96x256_w1x4_m32", 1},  // 24.24 / 25.09 us (96x256: 25.71 / 26.58; 128x256 m32: 25.81 / 27.15 before)
+    {2048, 2112, 7168, "bdirect_96x256_w1x4_m32", 1},  // 23.18 / 24.15 us (96x256: 24.67 / 25.28; 128x256 m32: 25.81 / 27.15 before)
     {1000, 1280, 512, "bdirect_64x128_w1x2", 1},  // 4.9 us
     {3333, 5120, 512, "bdirect_64x128_w1x2", 1},  // 15.3 us
     {1000, 5120, 12288, "bdirect_96x256_w1x4", 1},  // 39.21 / 40.25 us (96x256 m32: 40.85 / 41.23; 128x256 m32: 42.22 / 42.28)
-    {3333, 1280, 12288, "bdirect_96x256_w1x4_m32", 1},  // 34.72 / 36.10 us (96x256: 36.67 / 37.24; 128x256 m32: 39.16 / 40.76 before)
+    {3333, 1280, 12288, "bdirect_96x256_w1x4_m32", 1},  // 33.48 / 34.73 us (96x256: 34.75 / 35.77; 128x256 m32: 39.16 / 40.76 before)
     {8192, 10240, 5120, "bdirect_256x256_w2x2", 1},  // 186.5 us
-    {8192, 17408, 5120, "bdirect_192x256_w1x4", 1},  // 327.5 us
+    {8192, 17408, 5120, "bdirect_192x256_w1x4", 1},  // 307.3 / 317.7 us (2x2: 313.1 / 320.9)
     {8192, 5120, 17408, "bdirect_256x256_w2x2", 1},  // 295.7 us
-    {8192, 12288, 5120, "bdirect_256x256_w1x4", 1},  // 238.0 / 235.8 us (128x384: 258.7 / 249.6)
+    {8192, 12288, 5120, "bdirect_256x256_w1x4", 1},  // 204.3 / 209.3 us (2x2: 205.4 / 211.6)
     {8192, 8192, 8192, "bdirect_256x256_w2x2", 1},  // 219.7 us
     {128, 256, 512, "bdirect_64x64_w1x1", 1},  // 4.5 us
     {4096, 4096, 4096, "bdirect_256x256_w2x2", 1},  // 35.3 us
