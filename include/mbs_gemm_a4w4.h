@@ -126,7 +126,9 @@ int mbs_gemm_a4w4_launch_noalloc(int config, int splits, const uint8_t* A, const
  * scales come in 32-row groups).  mbs_gemm_a4w4_check_groups reports both
  * cases.  Rows past group_offsets[E] are not written.
  * config: -1 for the heuristic, else 0 <= config <
- * mbs_gemm_a4w4_grouped_num_configs().  Each expert's rows give the same
+ * mbs_gemm_a4w4_grouped_num_configs(); the configurations named *_m32
+ * (32x32x64-MFMA tiles) need K % 512 == 0 and return MBS_ERR_CONFIG
+ * otherwise, before any launch.  Each expert's rows give the same
  * bytes as mbs_gemm_a4w4_launch on that expert alone.  No counterpart in the
  * reference (its launcher takes one weight matrix). */
 int mbs_gemm_a4w4_grouped_launch(const uint8_t* A, const uint8_t* B, const uint8_t* AScale,
@@ -166,7 +168,9 @@ size_t mbs_gemm_a4w4_workspace_bytes(int M, int N, int K);
  * (kernel family, tile, split) triple; mbs_gemm_a4w4_plan_name() describes
  * the one the heuristic picks for (M,N,K).  mbs_gemm_a4w4_launch_config()
  * runs kernel configuration `config` (0 <= config < mbs_gemm_a4w4_num_configs())
- * with `splits` K-splits (0 = the heuristic's choice for that config).
+ * with `splits` K-splits (0 = the heuristic's choice for that config).  The
+ * configurations named *_m32 (32x32x64-MFMA tiles) run K % 512 == 0 with one
+ * split only and return MBS_ERR_CONFIG otherwise, before any launch.
  * Stands in for the reference's MBS_FORCE_TILE_ENV / MBS_TILE debug switch
  * (kernel/gemm_a4w4.hip:1094-1102). */
 int mbs_gemm_a4w4_num_configs(void);
