@@ -122,6 +122,8 @@ def phase_lib():
     P, I, S = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
     L.mbs_gemm_a4w4_launch.argtypes = [P, P, P, P, P, P, P, I, I, I, I, I, P, S, P]
     L.mbs_gemm_a4w4_launch.restype = I
+    L.mbs_gemm_a4w4_launch_config.argtypes = [I, I, P, P, P, P, P, P, P, I, I, I, I, I, P, S, P]
+    L.mbs_gemm_a4w4_launch_config.restype = I
     L.mbs_gemm_a4w4_workspace_bytes.argtypes = [I, I, I]
     L.mbs_gemm_a4w4_workspace_bytes.restype = S
     L.mbs_phase_timer_attach.argtypes = [P]
@@ -132,11 +134,12 @@ def phase_lib():
 PHASES = ("prologue", "stage_wait", "barrier", "stage_body", "epilogue", "next_unit")
 
 
-def phase_split(ops, M, N, K, launches=20):
+def phase_split(ops, M, N, K, launches=20, config=None):
     """In-kernel cycle split of the persistent GEMM on operands `ops` (the
     phase-timer build: s_memtime per phase per wave), with the shader clock
     from s_memtime / s_memrealtime and the kernel time with and without the
-    timer (HIP events, eager launches)."""
+    timer (HIP events, eager launches).  `config`: a persistent configuration
+    name to force (one split) instead of the planner's plan."""
     import ctypes
 
     import torch
@@ -157,9 +160,19 @@ def phase_split(ops, M, N, K, launches=20):
     p = lambda t: ctypes.c_void_p(t.data_ptr())
     strm = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
+    cfg = -1
+    if config:
+        L.mbs_gemm_a4w4_config_name.restype = ctypes.c_char_p
+        names = [L.mbs_gemm_a4w4_config_name(i).decode() for i in range(L.mbs_gemm_a4w4_num_configs())]
+        cfg = names.index(config)
+
     def call():
-        st = L.mbs_gemm_a4w4_launch(p(A), p(B), p(As), p(Bs), None, None, p(out), M, N, K, Mpad, snp,
-                                    p(ws), wsb, strm())
+        if cfg >= 0:
+            st = L.mbs_gemm_a4w4_launch_config(cfg, 1, p(A), p(B), p(As), p(Bs), None, None, p(out), M, N, K,
+                                               Mpad, snp, p(ws), wsb, strm())
+        else:
+            st = L.mbs_gemm_a4w4_launch(p(A), p(B), p(As), p(Bs), None, None, p(out), M, N, K, Mpad, snp,
+                                        p(ws), wsb, strm())
         assert st == 0, st
 
     def timed(n):
@@ -184,7 +197,7 @@ def phase_split(ops, M, N, K, launches=20):
     total = sum(cyc.values())
     stages, units, clk, rt = v[len(PHASES):len(PHASES) + 4]
     res = {
-        "shape": [M, N, K], "plan": mbs_amd.ext().plan_name(M, N, K), "launches": launches,
+        "shape": [M, N, K], "plan": config or mbs_amd.ext().plan_name(M, N, K), "launches": launches,
         "kernel_us_plain": round(us_plain, 2), "kernel_us_timed": round(us_timed, 2),
         "sclk_mhz": round(clk / rt * 100.0, 1) if rt else None,
         "wave_cycles": total,
@@ -524,6 +537,8 @@ def main():
     ap.add_argument("--phase-split", action="store_true",
                     help="only print the in-kernel phase split of configs[1] (or --shape) from "
                          "the phase-timer build")
+    ap.add_argument("--config", type=str, default="",
+                    help="with --phase-split: force this persistent configuration (by name, one split)")
     ap.add_argument("--sustain", type=int, default=0, metavar="N",
                     help="only run N back-to-back eager launches of configs[1] after 1 s idle and "
                          "print their event times (for a kernel trace of the clock's response)")
@@ -588,7 +603,7 @@ def main():
     if args.phase_split:
         M, N, K = (int(v) for v in args.shape.split(",")) if args.shape else (8192, 8192, 8192)
         ops, _ = prepare(M, N, K, 1, dev)
-        print(json.dumps({"phase_split": phase_split(ops, M, N, K)}), flush=True)
+        print(json.dumps({"phase_split": phase_split(ops, M, N, K, config=args.config or None)}), flush=True)
         return
     M = N = K = 8192
     (A, B, As, Bs), (x, w) = prepare(M, N, K, 1, dev)
