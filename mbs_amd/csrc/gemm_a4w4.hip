@@ -312,7 +312,9 @@ double plan_cost(const Plan& pl, int M, int N, int K)
 // rounds) after the 96-row tiles' A DMAs were dealt without fillers and the
 // stage-top waits relaxed, which made the 96-row tiles 11-19% faster in
 // all (their stage cost above is scaled by 0.87); six entries again after
-// the pipelined epilogue (2 x 7 rounds; "before": not re-measured).
+// the pipelined epilogue (2 x 7 rounds; "before": not re-measured), and the
+// three with fewer tiles than workgroup slots (1000, 3333 and 2048 x 2112
+// rows) after their grids got the XCD remap.
 struct TunedPlan {
     int M, N, K;
     const char* config;
@@ -326,11 +328,11 @@ const TunedPlan kTuned[] = {
     {256, 4096, 7168, "bdirect_64x128_w1x2", 1},  // 13.1 us
     {2048, 4096, 7168, "bdirect_128x256_w1x4_m32", 1},  // 32.17 / 33.43 us (128x256 1x4: 33.06 / 33.61; 96x256: 42.51 / 44.62 before)
     {256, 2112, 7168, "bdirect_64x128_w1x2", 2},  // 13.1 us
-    {2048, 2112, 7168, "bdirect_96x256_w1x4_m32", 1},  // 23.18 / 24.15 us (96x256: 24.67 / 25.28; 128x256 m32: 25.81 / 27.15 before)
+    {2048, 2112, 7168, "bdirect_96x256_w1x4_m32", 1},  // 22.76 / 23.57 us (96x256: 24.05 / 25.41)
     {1000, 1280, 512, "bdirect_64x128_w1x2", 1},  // 4.9 us
     {3333, 5120, 512, "bdirect_64x128_w1x2", 1},  // 15.3 us
-    {1000, 5120, 12288, "bdirect_96x256_w1x4", 1},  // 39.21 / 40.25 us (96x256 m32: 40.85 / 41.23; 128x256 m32: 42.22 / 42.28)
-    {3333, 1280, 12288, "bdirect_96x256_w1x4_m32", 1},  // 33.48 / 34.73 us (96x256: 34.75 / 35.77; 128x256 m32: 39.16 / 40.76 before)
+    {1000, 5120, 12288, "bdirect_96x256_w1x4", 1},  // 36.67 / 37.82 us (96x256 m32: 37.12 / 38.05; 128x256 m32: 39.72 / 42.20)
+    {3333, 1280, 12288, "bdirect_96x256_w1x4_m32", 1},  // 33.80 / 34.78 us (96x256: 35.83 / 36.99)
     {8192, 10240, 5120, "bdirect_256x256_w2x2", 1},  // 186.5 us
     {8192, 17408, 5120, "bdirect_192x256_w1x4", 1},  // 307.3 / 317.7 us (2x2: 313.1 / 320.9)
     {8192, 5120, 17408, "bdirect_256x256_w2x2", 1},  // 295.7 us

@@ -386,7 +386,10 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
     // With G % 8 == 0 the ids of one XCD are those with id % 8 == x; map
     // them onto a contiguous range of units so that the units an XCD runs
     // concurrently form a compact block of tiles (GROUP tile-rows tall).
-    const bool remap = (G & 7) == 0;
+    // With at most one unit per workgroup (units <= G) each workgroup's only
+    // unit is its own id, so the map also holds for any G (the units past
+    // the last multiple of 8 keep their ids).
+    const bool remap = (G & 7) == 0 || units <= G;
     const int units8 = units & ~7;
     auto unit_of = [&](int id) __attribute__((always_inline)) {
         Unit u;
