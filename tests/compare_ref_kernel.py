@@ -4,14 +4,15 @@ kernel (built from its sources into oracle/_ref/libref_gemm.so by
 oracle/Makefile), on identical operand bytes.  Test infrastructure: run by
 hand on a GPU box, not collected by pytest.
 
-    python tests/compare_ref_kernel.py [--replays 20]
+    python tests/compare_ref_kernel.py [--replays 10] [--rounds 7]
 
 For every shape both launchers get the same A, B, scales (and factors where
 the reference's workgroup path needs them: kernel/gemm_a4w4.hip:1044-1146
 takes its factor pointers unconditionally there), the outputs are compared
 against each other with the north-star tolerance, and each launcher is timed
-by HIP-graph replay (one graph of `copies` launches, replayed `replays`
-times).  Decode shapes rotate ten weight copies (cold: more bytes than the
+by HIP-graph replay (one graph of `copies` launches; a timed block replays it
+`replays` times; `rounds` interleaved rounds of one block per launcher, the
+order alternating; medians).  Decode shapes rotate ten weight copies (cold: more bytes than the
 MALL); large shapes reuse one copy, as the reference's own measurement does
 (asm_vs_wg_kernel.md:179-180).  Prints one JSON object per shape.
 
@@ -28,6 +29,7 @@ import argparse
 import ctypes
 import json
 import os
+import statistics
 import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -64,7 +66,8 @@ SHAPES = [
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--replays", type=int, default=20)
+    ap.add_argument("--replays", type=int, default=10, help="graph replays per timed block")
+    ap.add_argument("--rounds", type=int, default=7, help="interleaved rounds (median)")
     ap.add_argument("--only", type=str, default="", help="comma list of MxNxK to run")
     ap.add_argument("--eager", type=int, default=0, metavar="N",
                     help="N synchronised eager launches of each kernel, no timing (counter runs)")
@@ -164,12 +167,17 @@ def main():
             torch.cuda.empty_cache()
             continue
 
-        def graph_time(launch):
+        def make_graph(launch):
             torch.cuda.synchronize()
             gr = torch.cuda.CUDAGraph()
             with torch.cuda.graph(gr):
                 for i in range(copies):
                     launch(i)
+            gr.replay()
+            torch.cuda.synchronize()
+            return gr
+
+        def block_time(gr):
             gr.replay()
             torch.cuda.synchronize()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -180,10 +188,16 @@ def main():
             torch.cuda.synchronize()
             return e0.elapsed_time(e1) * 1e3 / (args.replays * copies)
 
-        t_ref, t_own = graph_time(launch_ref), graph_time(launch_own)
-        # second pair, reversed order, to spread clock drift over both
-        t_own = min(t_own, graph_time(launch_own))
-        t_ref = min(t_ref, graph_time(launch_ref))
+        # Interleaved rounds, the order alternating, medians: the shader clock
+        # follows the load (power management), so blocks timed back to back
+        # in a fixed order would favour whichever kernel runs first.
+        g_ref, g_own = make_graph(launch_ref), make_graph(launch_own)
+        ts = {"ref": [], "own": []}
+        for r in range(args.rounds):
+            for k in (("ref", "own") if r % 2 == 0 else ("own", "ref")):
+                ts[k].append(block_time(g_ref if k == "ref" else g_own))
+        t_ref, t_own = statistics.median(ts["ref"]), statistics.median(ts["own"])
+        del g_ref, g_own
         flops = 2.0 * M * N * K
         byts = M * K // 2 + N * K // 2 + (M + N) * K // 32 + 2 * M * N
         buf = ctypes.create_string_buffer(128)
