@@ -266,7 +266,9 @@ def decode_bench(dev, Ms=(1, 4, 16, 32), N=8192, K=8192, copies=10, replays=20):
     """Cold (rotating copies) and warm per-launch time of the decode shapes,
     from HIP-graph replay so host launch overhead is excluded.  Also, cold,
     the reference's decode flow from a bf16 activation: quantize_mxfp4, then
-    gemm_a4w4 (two launches)."""
+    gemm_a4w4 (two launches), and the same product in one launch
+    (gemm_a4w4_from_bf16(one_launch=True): the decode kernel quantizes in
+    registers)."""
     import torch
 
     import mbs_amd
@@ -283,10 +285,13 @@ def decode_bench(dev, Ms=(1, 4, 16, 32), N=8192, K=8192, copies=10, replays=20):
     for M in Ms:
         (A, _, As, _), (xh, _) = prepare(M, 16, K, 2, dev)
         x = xh.to(dev)
-        for mode in ("cold", "warm", "quantize+gemm"):
+        for mode in ("cold", "warm", "quantize+gemm", "one_launch"):
             idx = [0] * copies if mode == "warm" else list(range(copies))
             if mode == "quantize+gemm":
                 run = lambda: [two_step(x, Bc[i], Bsc[i]) for i in idx]
+            elif mode == "one_launch":
+                run = lambda: [mbs_amd.gemm_a4w4_from_bf16(x, Bc[i], Bsc[i], one_launch=True)
+                               for i in idx]
             else:
                 run = lambda: [mbs_amd.gemm_a4w4(A, Bc[i], As, Bsc[i]) for i in idx]
             run()
@@ -304,8 +309,8 @@ def decode_bench(dev, Ms=(1, 4, 16, 32), N=8192, K=8192, copies=10, replays=20):
             torch.cuda.synchronize()
             us = e0.elapsed_time(e1) * 1e3 / (replays * copies)
             gbs = algo_bytes(M, N, K) / (us * 1e-6) / 1e9
-            if mode == "quantize+gemm":
-                res.setdefault(f"M={M}", {})["cold_quantize+gemm_us"] = round(us, 3)
+            if mode in ("quantize+gemm", "one_launch"):
+                res.setdefault(f"M={M}", {})[f"cold_{mode}_us"] = round(us, 3)
             else:
                 res.setdefault(f"M={M}", {})[mode] = {
                     "us": round(us, 3), "GBps": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}

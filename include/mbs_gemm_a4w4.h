@@ -183,6 +183,32 @@ int mbs_gemm_a4w4_launch_config(int config, int splits, const uint8_t* A, const 
                                 int M, int N, int K, int Mpad, int scaleN_pad,
                                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* Decode GEMM from a bf16 activation in one launch:  x bf16 [M, K] (row
+ * stride K, 16-byte aligned), M <= 32, is quantized to MXFP4 inside the
+ * decode kernel (the rule of mbs_quantize_mxfp4_bf16, in registers; nothing
+ * is written back) and multiplied by B as in mbs_gemm_a4w4_launch_ex with no
+ * factors:  out[m][n] = bf16(C[m][n] * alpha + bias[n]).  The output bytes
+ * equal mbs_quantize_mxfp4_bf16 (shuffled scales) followed by
+ * mbs_gemm_a4w4_launch_ex on the same decode plan: config < 0 takes the
+ * plan the heuristic picks among the skinny (decode) configurations, the
+ * one mbs_gemm_a4w4_launch runs for these shapes; config >= 0 must name a
+ * skinny configuration (MBS_ERR_CONFIG otherwise), with `splits` as in
+ * mbs_gemm_a4w4_launch_config.  M > 32 returns MBS_ERR_ARGUMENT.  Split-K
+ * plans use `workspace` (size it with mbs_gemm_a4w4_from_bf16_workspace_bytes
+ * or, for a forced config, mbs_gemm_a4w4_config_workspace_bytes).  Replaces
+ * the two launches of the reference's decode flow, aiter's per_1x32 quantizer
+ * then gemm_a4w4 (test_gemm_a4w4.py:134-141, bench_one.py:19-30); the
+ * reference has no fused form.  Every workgroup quantizes the rows it needs
+ * itself: for M <= 4 (only the live rows' blocks) this is faster than the two
+ * launches; for larger M each workgroup re-quantizes 16 or 32 rows and the
+ * two launches are faster (measured at N = K = 8192 on MI355X). */
+int mbs_gemm_a4w4_from_bf16_launch(int config, int splits, const void* x, const uint8_t* B,
+                                   const uint8_t* BScale, void* out, int M, int N, int K,
+                                   int Mpad, int scaleN_pad, float alpha, const void* bias,
+                                   void* workspace, size_t workspace_bytes, void* stream);
+/* Workspace the heuristic (config < 0) bf16-activation launch wants. */
+size_t mbs_gemm_a4w4_from_bf16_workspace_bytes(int M, int N, int K);
+
 /* ---------------------------------------------------------------- formats
  * The on-device format helpers the reference takes from aiter
  * (test_gemm_a4w4.py:134-141): quantize, preshuffle, dequantize.

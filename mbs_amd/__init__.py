@@ -77,6 +77,21 @@ def gemm_a4w4(A, B, A_scale, B_scale, A_factor=None, B_factor=None, alpha: float
     return ext().gemm_a4w4(A, B, A_scale, B_scale, A_factor, B_factor, alpha, bias)
 
 
+def gemm_a4w4_from_bf16(x, B, B_scale, alpha: float = 1.0, bias=None, config: int = -1,
+                        splits: int = 0, one_launch=None):
+    """out[M,N] bf16 from a bf16 activation x [M,K]: the reference's decode
+    flow, the per_1x32 quantizer then ``gemm_a4w4`` (test_gemm_a4w4.py:134-141,
+    bench_one.py:19-30), with the same output bytes as quantizing x with
+    ``quantize_mxfp4`` and calling ``gemm_a4w4`` on the result.  It runs in
+    one launch (the decode kernel quantizes x in registers) for M <= 4, where
+    that is faster, and as the two launches otherwise; ``one_launch=True``
+    forces the one-launch form (M <= 32), ``False`` the two launches.
+    ``config``/``splits`` force a skinny (decode) configuration of the
+    one-launch form."""
+    mode = -1 if one_launch is None else int(bool(one_launch))
+    return ext().gemm_a4w4_from_bf16(x, B, B_scale, alpha, bias, config, splits, mode)
+
+
 def gemm_a4w4_grouped(A, B, A_scale, B_scale, group_offsets, A_factor=None, B_factor=None,
                       config: int = -1, alpha: float = 1.0, bias=None, validate: bool = False):
     """Grouped (mixture-of-experts) GEMM in one launch.

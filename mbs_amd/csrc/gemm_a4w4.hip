@@ -17,7 +17,9 @@
 //  * gemm_skinny_kernel -- decode shapes (M <= 32): each wave streams 16 or
 //    32 rows of B (non-temporal) straight into VGPRs with a batch of its
 //    K-chunk in flight, reusing each A fragment for every B fragment; waves
-//    of a workgroup split K and reduce through LDS in a fixed order.
+//    of a workgroup split K and reduce through LDS in a fixed order.  Its
+//    bf16-activation form quantizes A in registers (one launch from a bf16
+//    activation, mbs_gemm_a4w4_from_bf16_launch).
 //  * splitk_reduce_kernel -- deterministic fixed-order sum of fp32 split-K
 //    partials plus the same epilogue.
 #include "gemm_kernels.h"
@@ -144,6 +146,8 @@ struct Config {
     // whole K only: no K tail, no dead stages (K % 512 == 0), one split
     // (the 32x32x64 MFMA tiles)
     bool whole_k = false;
+    // skinny: the same plan with A given as bf16, quantized in registers
+    hipError_t (*launch_xbf)(const GemmArgs&, dim3, bool, bool, hipStream_t) = nullptr;
 };
 
 const Config kConfigs[] = {
@@ -169,13 +173,13 @@ const Config kConfigs[] = {
     {"bdirect_128x384_w1x4_m32", kPersistent, 128, 384, 256, 1, {0.455f, 0.455f, 4.55f}, launch_bdirect<B128x384m>, true, true},
     // skinny: bm = rows covered (16*MT), bn = B rows per workgroup (16*NF)
     // eff = streaming efficiency relative to the best variant (cold N=K=8192 timings)
-    {"skinny_m16_n32_w16", kSkinny, 16, 32, 1024, 1, {0.94f, 0.f, 0.f}, launch_skinny<1, 2, 16, 4>},
-    {"skinny_m32_n32_w16", kSkinny, 32, 32, 1024, 1, {0.89f, 0.f, 0.f}, launch_skinny<2, 2, 16, 4>},
-    {"skinny_m16_n32_w8", kSkinny, 16, 32, 512, 2, {1.00f, 0.f, 0.f}, launch_skinny<1, 2, 8, 4>},
-    {"skinny_m32_n32_w8", kSkinny, 32, 32, 512, 2, {0.92f, 0.f, 0.f}, launch_skinny<2, 2, 8, 4>},
-    {"skinny_m16_n16_w8", kSkinny, 16, 16, 512, 2, {0.91f, 0.f, 0.f}, launch_skinny<1, 1, 8, 8>},
-    {"skinny_m32_n16_w8", kSkinny, 32, 16, 512, 2, {0.69f, 0.f, 0.f}, launch_skinny<2, 1, 8, 8>},
-    {"skinny_m32_n32_w4", kSkinny, 32, 32, 256, 2, {1.00f, 0.f, 0.f}, launch_skinny<2, 2, 4, 4>},
+    {"skinny_m16_n32_w16", kSkinny, 16, 32, 1024, 1, {0.94f, 0.f, 0.f}, launch_skinny<1, 2, 16, 4>, false, false, launch_skinny_xbf<1, 2, 16, 4>},
+    {"skinny_m32_n32_w16", kSkinny, 32, 32, 1024, 1, {0.89f, 0.f, 0.f}, launch_skinny<2, 2, 16, 4>, false, false, launch_skinny_xbf<2, 2, 16, 4>},
+    {"skinny_m16_n32_w8", kSkinny, 16, 32, 512, 2, {1.00f, 0.f, 0.f}, launch_skinny<1, 2, 8, 4>, false, false, launch_skinny_xbf<1, 2, 8, 4>},
+    {"skinny_m32_n32_w8", kSkinny, 32, 32, 512, 2, {0.92f, 0.f, 0.f}, launch_skinny<2, 2, 8, 4>, false, false, launch_skinny_xbf<2, 2, 8, 4>},
+    {"skinny_m16_n16_w8", kSkinny, 16, 16, 512, 2, {0.91f, 0.f, 0.f}, launch_skinny<1, 1, 8, 8>, false, false, launch_skinny_xbf<1, 1, 8, 8>},
+    {"skinny_m32_n16_w8", kSkinny, 32, 16, 512, 2, {0.69f, 0.f, 0.f}, launch_skinny<2, 1, 8, 8>, false, false, launch_skinny_xbf<2, 1, 8, 8>},
+    {"skinny_m32_n32_w4", kSkinny, 32, 32, 256, 2, {1.00f, 0.f, 0.f}, launch_skinny<2, 2, 4, 4>, false, false, launch_skinny_xbf<2, 2, 4, 4>},
 };
 constexpr int kNumConfigs = (int)(sizeof(kConfigs) / sizeof(kConfigs[0]));
 constexpr int kNumCUs = 256;
@@ -352,11 +356,14 @@ int config_index(const char* name)
     return -1;
 }
 
-bool choose_plan(int M, int N, int K, size_t ws_avail, Plan* best)
+// skinny_only: choose among the decode (skinny) configurations only; for a
+// shape whose unrestricted choice is skinny this is the same plan.
+bool choose_plan(int M, int N, int K, size_t ws_avail, Plan* best, bool skinny_only = false)
 {
     for (const TunedPlan& t : kTuned) {
         if (t.M != M || t.N != N || t.K != K) continue;
         const int c = config_index(t.config);
+        if (skinny_only && (c < 0 || kConfigs[c].family != kSkinny)) continue;
         Plan pl;
         if (c >= 0 && make_plan(c, t.splits, M, N, K, &pl) && pl.ws_bytes <= ws_avail) {
             *best = pl;
@@ -367,6 +374,7 @@ bool choose_plan(int M, int N, int K, size_t ws_avail, Plan* best)
     double best_cost = 0;
     for (int i = 0; i < kNumConfigs; ++i) {
         const bool skinny = kConfigs[i].family == kSkinny;
+        if (skinny_only && !skinny) continue;
         for (int want : {0, 1, 2, 4, 8}) {
             if (skinny != (want == 0)) continue;  // skinny: its own split rule
             Plan pl;
@@ -427,12 +435,32 @@ int validate(const uint8_t* A, const uint8_t* B, const uint8_t* As, const uint8_
     return MBS_OK;
 }
 
+// Arguments of the bf16-activation entry: x (bf16 [M, K]) takes the place
+// of A and its scales; decode shapes only.
+int validate_from_bf16(const void* x, const uint8_t* B, const uint8_t* Bs, void* out, int M,
+                       int N, int K, int Mpad, int snp)
+{
+    if (M > 32)
+        return fail(MBS_ERR_ARGUMENT, "the bf16-activation GEMM takes M <= 32 (decode shapes), got M=" +
+                                          std::to_string(M));
+    if (M > 0 && !x) return fail(MBS_ERR_ARGUMENT, "null activation pointer");
+    if (misaligned(x, 16)) return fail(MBS_ERR_ARGUMENT, "x must be 16-byte aligned");
+    // The remaining checks are the packed entry's (x stands in for A and its
+    // scale pointer; 32 rows of bf16 x stay below 2^31 bytes whenever the
+    // K limit there holds).
+    const uint8_t* xa = static_cast<const uint8_t*>(x);
+    return validate(xa, B, xa, Bs, nullptr, nullptr, out, M, N, K, Mpad, snp);
+}
+
+// xbf: A is bf16 [M, K] quantized in registers (skinny plans only).
 int run_plan(const Plan& pl, const uint8_t* A, const uint8_t* B, const uint8_t* As,
              const uint8_t* Bs, const uint8_t* Af, const uint8_t* Bf, void* out, int M, int N,
              int K, int snp, void* ws, size_t ws_bytes, void* stream, float alpha = 1.0f,
-             const void* bias = nullptr)
+             const void* bias = nullptr, bool xbf = false)
 {
     const Config& c = kConfigs[pl.config];
+    if (xbf && !c.launch_xbf)
+        return fail(MBS_ERR_CONFIG, std::string(c.name) + " has no bf16-activation variant");
     if (pl.ws_bytes > ws_bytes || (pl.ws_bytes && !ws))
         return fail(MBS_ERR_WORKSPACE, "workspace too small: need " + std::to_string(pl.ws_bytes) +
                                            " bytes");
@@ -459,7 +487,7 @@ int run_plan(const Plan& pl, const uint8_t* A, const uint8_t* B, const uint8_t* 
     const int S_total = stages_of(K);
     const bool ktail = (K % 128) != 0;
     const bool gen = c.persistent ? (ktail || pl.sps % 4 != 0 || S_total % pl.sps != 0) : ktail;
-    hipError_t e = c.launch(a, pl.grid, gen, pl.splits > 1, s);
+    hipError_t e = (xbf ? c.launch_xbf : c.launch)(a, pl.grid, gen, pl.splits > 1, s);
     if (e != hipSuccess) return fail(MBS_ERR_LAUNCH, std::string("launch failed: ") + hipGetErrorString(e));
     if (pl.splits > 1) {
         const int64_t quads = (int64_t)M * (N / 4);
@@ -770,6 +798,40 @@ int mbs_gemm_a4w4_launch_ex(int config, int splits, const uint8_t* A, const uint
     }
     return run_plan(pl, A, B, AScale, BScale, AFactor, BFactor, out, M, N, K, scaleN_pad,
                     workspace, workspace_bytes, stream, alpha, bias);
+}
+
+size_t mbs_gemm_a4w4_from_bf16_workspace_bytes(int M, int N, int K)
+{
+    if (M < 1 || M > 32 || N < 16 || K < 64 || N % 16 || K % 64) return 0;
+    Plan pl;
+    if (!choose_plan(M, N, K, (size_t)1 << 31, &pl, true)) return 0;
+    return pl.ws_bytes;
+}
+
+int mbs_gemm_a4w4_from_bf16_launch(int config, int splits, const void* x, const uint8_t* B,
+                                   const uint8_t* BScale, void* out, int M, int N, int K,
+                                   int Mpad, int scaleN_pad, float alpha, const void* bias,
+                                   void* workspace, size_t workspace_bytes, void* stream)
+{
+    set_last_error("");
+    int st = validate_from_bf16(x, B, BScale, out, M, N, K, Mpad, scaleN_pad);
+    if (st != MBS_OK) return st;
+    if (!(alpha == alpha)) return fail(MBS_ERR_ARGUMENT, "alpha is NaN");
+    if (config >= kNumConfigs || (config >= 0 && kConfigs[config].family != kSkinny))
+        return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) +
+                                        " is not a decode (skinny) configuration");
+    if (M == 0) return MBS_OK;
+    Plan pl;
+    if (config < 0) {
+        if (!choose_plan(M, N, K, workspace ? workspace_bytes : 0, &pl, true))
+            return fail(MBS_ERR_CONFIG, "no decode configuration fits this problem");
+    } else if (!make_plan(config, splits, M, N, K, &pl)) {
+        return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) + " cannot run M=" +
+                                        std::to_string(M) + " K=" + std::to_string(K) + " with " +
+                                        std::to_string(splits) + " splits");
+    }
+    return run_plan(pl, static_cast<const uint8_t*>(x), B, nullptr, BScale, nullptr, nullptr, out,
+                    M, N, K, scaleN_pad, workspace, workspace_bytes, stream, alpha, bias, true);
 }
 
 #if MBS_PHASE_TIMER

@@ -419,6 +419,70 @@ at::Tensor gemm_a4w4_grouped(at::Tensor A, at::Tensor B, at::Tensor A_scale, at:
     return out.narrow(0, 0, M);
 }
 
+// Decode from a bf16 activation, x bf16 [M, K]: one launch (the decode
+// kernel quantizes x in registers, M <= 32) or two (quantize_mxfp4, then
+// gemm_a4w4).  Either way the bytes are those of quantize_mxfp4 followed by
+// gemm_a4w4 on the same plan.  one_launch: 1 forces the one-launch form, 0
+// the two launches, -1 picks the faster: one launch for M <= 4 (each
+// workgroup quantizes the live rows only: 7.6 / 8.3 us against 9.7 / 9.8 us
+// for two launches at M = 1 / 4, N = K = 8192, cold, MI355X), two launches
+// above (every workgroup re-quantizes all 16 or 32 rows of A: at M = 16 / 32
+// one launch takes longer than two).  config/splits force a skinny
+// configuration (one launch only; -1: the heuristic's).
+constexpr int64_t kOneLaunchMaxM = 4;
+
+at::Tensor gemm_a4w4_from_bf16(at::Tensor x, at::Tensor B, at::Tensor B_scale, double alpha,
+                               c10::optional<at::Tensor> bias, int64_t config, int64_t splits,
+                               int64_t one_launch)
+{
+    TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.scalar_type() == at::kBFloat16,
+                "gemm_a4w4_from_bf16: x must be a 2D bf16 device tensor");
+    const bool one = one_launch > 0 || config >= 0 || (one_launch < 0 && x.size(0) <= kOneLaunchMaxM);
+    TORCH_CHECK(!(one && x.size(0) > 32), "gemm_a4w4_from_bf16: the one-launch form needs M <= 32");
+    TORCH_CHECK(!(one_launch == 0 && config >= 0),
+                "gemm_a4w4_from_bf16: a forced config runs the one-launch form");
+    if (!one) {
+        auto q = quantize_mxfp4(x, true, 127);
+        return run(prepare(std::get<0>(q), B, std::get<1>(q), B_scale, c10::nullopt, c10::nullopt),
+                   -1, 0, alpha, bias);
+    }
+    TORCH_CHECK(B.is_cuda() && B.dim() == 2 && B_scale.is_cuda() && B.element_size() == 1 &&
+                    B_scale.element_size() == 1,
+                "gemm_a4w4_from_bf16: B and B_scale must be 1-byte device tensors, B 2D");
+    TORCH_CHECK(B.device() == x.device() && B_scale.device() == x.device(),
+                "gemm_a4w4_from_bf16: all operands must be on the same device");
+    auto xc = aligned_contiguous(x);
+    const at::Tensor Bb = as_bytes(B), Bsb = as_bytes(B_scale);
+    const int64_t M = xc.size(0), K = xc.size(1), N = Bb.size(0);
+    TORCH_CHECK(Bb.size(1) * 2 == K, "gemm_a4w4_from_bf16: B must be [N, K/2], got K/2 = ",
+                Bb.size(1), " for K = ", K);
+    TORCH_CHECK(Bsb.numel() >= round_up(N, 32) * scale_pad(K),
+                "gemm_a4w4_from_bf16: B_scale must hold at least ", round_up(N, 32) * scale_pad(K),
+                " bytes (round_up(N,32) * scaleN_pad), got ", Bsb.numel());
+    c10::DeviceGuard guard(x.device());
+    const int64_t Mpad = round_up(M, 32);
+    auto out = torch::empty({Mpad, N}, torch::TensorOptions().dtype(torch::kBFloat16).device(x.device()));
+    const size_t ws = config < 0 ? mbs_gemm_a4w4_from_bf16_workspace_bytes((int)M, (int)N, (int)K)
+                                 : mbs_gemm_a4w4_config_workspace_bytes((int)config, (int)splits,
+                                                                        (int)M, (int)N, (int)K);
+    at::Tensor wst;
+    if (ws) wst = torch::empty({(int64_t)ws}, torch::TensorOptions().dtype(torch::kByte).device(x.device()));
+    at::Tensor bu;
+    if (bias.has_value()) {
+        TORCH_CHECK(bias->is_cuda() && bias->device() == x.device() &&
+                        bias->scalar_type() == at::kBFloat16 && bias->numel() == N,
+                    "gemm_a4w4_from_bf16: bias must be a bf16 device tensor of N entries");
+        bu = aligned_contiguous(*bias);
+    }
+    check_status(mbs_gemm_a4w4_from_bf16_launch(
+                     (int)config, (int)splits, xc.data_ptr(), Bb.data_ptr<uint8_t>(),
+                     Bsb.data_ptr<uint8_t>(), out.data_ptr(), (int)M, (int)N, (int)K, (int)Mpad,
+                     (int)scale_pad(K), (float)alpha, bu.defined() ? bu.data_ptr() : nullptr,
+                     ws ? wst.data_ptr() : nullptr, ws, current_stream(x)),
+                 "gemm_a4w4_from_bf16");
+    return out.narrow(0, 0, M);
+}
+
 std::string plan_name(int64_t M, int64_t N, int64_t K)
 {
     char buf[256];
@@ -472,6 +536,13 @@ PYBIND11_MODULE(mbs_gemm_a4w4, m)
     m.def("grouped_num_configs", []() { return mbs_gemm_a4w4_grouped_num_configs(); });
     m.def("grouped_config_name",
           [](int64_t c) { return std::string(mbs_gemm_a4w4_grouped_config_name((int)c)); });
+    m.def("gemm_a4w4_from_bf16", &gemm_a4w4_from_bf16,
+          "GEMM from a bf16 activation: quantize_mxfp4(x) then gemm_a4w4, in one launch "
+          "for M <= 4 (or when asked, M <= 32)",
+          pybind11::arg("x"), pybind11::arg("B"), pybind11::arg("B_scale"),
+          pybind11::arg("alpha") = 1.0, pybind11::arg("bias") = pybind11::none(),
+          pybind11::arg("config") = -1, pybind11::arg("splits") = 0,
+          pybind11::arg("one_launch") = -1);
     m.def("plan_name", &plan_name, "kernel plan the heuristic picks for (M, N, K)");
     m.def("num_configs", []() { return mbs_gemm_a4w4_num_configs(); });
     m.def("config_name", [](int64_t c) { return std::string(mbs_gemm_a4w4_config_name((int)c)); });

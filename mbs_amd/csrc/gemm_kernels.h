@@ -1481,12 +1481,31 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
 // in a fixed order (deterministic), then the waves run the epilogue of the
 // NF*MT output fragments.  NF = 1 covers half a 32-row scale group; NF =
 // 2*G covers G whole groups (one B-scale dword per group and 256 K).
-template <int MT, int NF, int NWK, int U, bool SPLIT>
+// XBF: A is bf16 [M, K] (row stride K) and is quantized to MXFP4 in
+// registers: the MFMA's A operand of lane l (row l % 16, K bytes 16*(l/16)
+// of a 128-K stage) is exactly one 32-element block, so each lane loads its
+// block's 64 bytes, quantizes it with the rule of the quantizer kernel and
+// builds the scale operand from the bytes it computes, the ones the shuffled
+// scale layout would hold at the op_sel positions (row tile m, stage parity h
+// -> byte m + 2h).  The products equal quantizing A first and running the
+// XBF = 0 kernel on the same plan, bit for bit.  Every workgroup quantizes
+// all of A, so the quantizer's VALU work is repeated per workgroup; XBF = 2
+// (M <= 4, one row tile) quantizes only the live rows' blocks -- lane j takes
+// block (row j/16, stage (j/4)%4, K-block j%4) of a 4-stage batch -- and
+// moves codes and scale bytes to the MFMA lanes with ds_bpermute.
+template <int MT, int NF, int NWK, int U, bool SPLIT, int XBF = 0>
 __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
 {
     static_assert(U % 2 == 0, "batch must cover whole 256-K scale groups");
     static_assert(NF == 1 || NF % 2 == 0, "whole 32-row scale groups (or half of one)");
     constexpr int NG = (NF + 1) / 2;   // 32-row B-scale groups per workgroup
+    // Stages per batch.  XBF holds 16 registers of bf16 A per stage and row
+    // tile: at 4 waves per SIMD (128 registers a wave) the batch is cut to
+    // 4 fragments of A so nothing spills.  The accumulation order over the
+    // stages does not depend on the batch.
+    constexpr int UB = (XBF && NWK >= 8 && MT * U > 4) ? 4 / MT : U;
+    constexpr bool XC = XBF == 2;
+    static_assert(!XC || (MT == 1 && UB == 4), "compact bf16 A: one row tile, 4-stage batches");
     __shared__ f32x4 red[NWK][NF * MT][64];
 
     const int lane = threadIdx.x & 63;
@@ -1507,8 +1526,9 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
     const int nfrag = min(NF, (p.N - n0) >> 4);
     const uint32_t fstride = (uint32_t)K * 8;  // bytes of one 16-row fragment column
     const rsrc_t rB = make_rsrc(p.B + (size_t)(n0 >> 4) * fstride, (uint32_t)nfrag * fstride);
-    const rsrc_t rA = make_rsrc(p.A, (uint32_t)(p.M * Kp));
-    const rsrc_t rAs = make_rsrc(p.As, (uint32_t)(32 * p.snp));
+    // bf16 A (XBF): rows >= M read as zeros from outside the range
+    const rsrc_t rA = make_rsrc(p.A, (uint32_t)(p.M * (XBF ? 2 * K : Kp)));
+    const rsrc_t rAs = make_rsrc(p.As, XBF ? 0u : (uint32_t)(32 * p.snp));
     const int Npad = (p.N + 31) & ~31;
     const rsrc_t rBs = make_rsrc(p.Bs + (size_t)(n0 >> 5) * 32 * p.snp,
                                  (uint32_t)(min(NG * 32, Npad - ((n0 >> 5) << 5)) * p.snp));
@@ -1523,21 +1543,32 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
         static_for<MT>([&](auto m) { acc[f][m] = f32x4{0.f, 0.f, 0.f, 0.f}; });
     });
 
-    for (int st = my_begin; st < my_end; st += U) {
-        i32x4 b[U][NF], a[U][MT];
-        int sb[U / 2][NG], sa[U / 2];
+    for (int st = my_begin; st < my_end; st += UB) {
+        i32x4 b[UB][NF], a[UB][MT];
+        int sb[UB / 2][NG], sa[UB / 2];
+        i32x4 x[XBF == 1 ? UB : 1][XBF == 1 ? MT : 1][4];  // XBF 1: the lane's bf16 A blocks
+        i32x4 xc[4];                                        // XBF 2: block (lane/16, (lane/4)%4, lane%4)
+        if constexpr (XC) {
+            // first in the issue order: the quantization then waits for these
+            // (from L2) and not for the batch's B stream; rows >= M lie
+            // outside the range and read as zeros
+            const int s = st + ((lane >> 2) & 3), kb = lane & 3;
+            const bool zap = (ktail && s == S_total - 1 && kb >= 2) || s >= my_end;
+            const uint32_t o = (uint32_t)(((lane >> 4) * K + s * 128 + kb * 32) * 2);
+            static_for<4>([&](auto i) { xc[i] = load16(rA, zap ? kOOB : o + 16 * i); });
+        }
         // Scales first: loads return in issue order, so stage u's MFMAs then
         // wait only for stage u's B and A, and the MFMAs trail the stream
         // instead of starting after the whole batch has landed.
-        static_for<U / 2>([&](auto v) {
+        static_for<UB / 2>([&](auto v) {
             const int g = (st >> 1) + v;
             const bool ok = st + 2 * v < my_end;
             static_for<NG>([&](auto G) {
                 sb[v][G] = load4(rBs, ok ? (uint32_t)(G * 32 * p.snp + g * 256 + lane * 4) : kOOB);
             });
-            sa[v] = load4(rAs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
+            if constexpr (!XBF) sa[v] = load4(rAs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
         });
-        static_for<U>([&](auto u) {
+        static_for<UB>([&](auto u) {
             const int s = st + u;
             const bool ok = s < my_end;
             const bool zap = (ktail && s == S_total - 1 && hi_lane) || !ok;
@@ -1545,20 +1576,56 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
                 b[u][f] = load16nt(rB, zap ? kOOB : (uint32_t)(f * fstride + s * 1024 + lane * 16));
             });
             static_for<MT>([&](auto m) {
-                a[u][m] = load16(rA, zap ? kOOB
-                                         : (uint32_t)((16 * m + (lane & 15)) * Kp + s * 64 +
-                                                      (lane >> 4) * 16));
+                if constexpr (XC) {
+                } else if constexpr (XBF) {
+                    // a row tile wholly past M reads nothing (and is not quantized)
+                    const bool dead = zap || 16 * m >= p.M;
+                    const uint32_t o = (uint32_t)(((16 * m + (lane & 15)) * K + s * 128 + (lane >> 4) * 32) * 2);
+                    static_for<4>([&](auto i) { x[u][m][i] = load16(rA, dead ? kOOB : o + 16 * i); });
+                } else {
+                    a[u][m] = load16(rA, zap ? kOOB
+                                             : (uint32_t)((16 * m + (lane & 15)) * Kp + s * 64 +
+                                                          (lane >> 4) * 16));
+                }
             });
         });
         // Every load of the batch is issued before the first MFMA; left to
         // itself the scheduler interleaves them with the MFMAs and the wave
         // keeps only a fraction of its batch in flight.
         __builtin_amdgcn_sched_barrier(0);
-        static_for<U>([&](auto u) {
+        i32x4 qc;
+        uint32_t qe = 0;
+        if constexpr (XC) qc = quantize_block32(xc, &qe);
+        static_for<UB>([&](auto u) {
             constexpr int h = u & 1;
             const int s = st + u;
             const bool tail = ktail && s == S_total - 1 && hi_lane;
-            int sav = sa[u / 2];
+            int sav;
+            if constexpr (XC) {
+                // MFMA lane (row l%16, K-block l/16) <- lane 16*row + 4u + l/16;
+                // rows 4..15 are past M
+                const bool live = (lane & 15) < 4;
+                const int src = (((lane & 15) * 16 + 4 * u + (lane >> 4)) & 63) * 4;
+                static_for<4>([&](auto i) {
+                    constexpr int I = decltype(i)::value;
+                    const int v = __builtin_amdgcn_ds_bpermute(src, qc[I]);
+                    a[u][0][I] = live ? v : 0;
+                });
+                const uint32_t e = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)qe);
+                sav = live ? (int)(e << (16 * h)) : 0;
+            } else if constexpr (XBF) {
+                // this stage's blocks: codes into a[u][m], scales to byte m + 2h
+                uint32_t sq = 0;
+                static_for<MT>([&](auto m) {
+                    uint32_t e = 0;
+                    if (16 * m < p.M) a[u][m] = quantize_block32(x[u][m], &e);
+                    else a[u][m] = i32x4{0, 0, 0, 0};
+                    sq |= e << (8 * (m + 2 * h));
+                });
+                sav = (int)sq;
+            } else {
+                sav = sa[u / 2];
+            }
             sav = tail ? 0x7F7F7F7F : sav;
             static_for<NF>([&](auto f) {
                 int sbv = sb[u / 2][f / 2] >> sshift;
@@ -1665,6 +1732,23 @@ hipError_t launch_skinny(const GemmArgs& a, dim3 grid, bool, bool split, hipStre
     return hipGetLastError();
 }
 
+// The same plans with A given as bf16 and quantized in registers; one row
+// tile with M <= 4 takes the compact form.
+template <int MT, int NF, int NWK, int U>
+hipError_t launch_skinny_xbf(const GemmArgs& a, dim3 grid, bool, bool split, hipStream_t s)
+{
+    if constexpr (MT == 1) {
+        if (a.M <= 4) {
+            if (split) hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, true, 2>), grid, dim3(64 * NWK), 0, s, a);
+            else hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, false, 2>), grid, dim3(64 * NWK), 0, s, a);
+            return hipGetLastError();
+        }
+    }
+    if (split) hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, true, 1>), grid, dim3(64 * NWK), 0, s, a);
+    else hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, false, 1>), grid, dim3(64 * NWK), 0, s, a);
+    return hipGetLastError();
+}
+
 using B256x256 = BdShape<256, 256, 2, 2>;
 using B256x128 = BdShape<256, 128, 2, 2>;
 using B128x256 = BdShape<128, 256, 2, 2>;
@@ -1699,10 +1783,14 @@ using B128x384m = BdShape<128, 384, 1, 4, true>;
 
 #define MBS_LAUNCH_SIG const GemmArgs&, dim3, bool, bool, hipStream_t
 #define MBS_BDIRECT_INST(T) template hipError_t launch_bdirect<T>(MBS_LAUNCH_SIG);
-#define MBS_SKINNY_INST(a, b, c, d) template hipError_t launch_skinny<a, b, c, d>(MBS_LAUNCH_SIG);
+#define MBS_SKINNY_INST(a, b, c, d)                                 \
+    template hipError_t launch_skinny<a, b, c, d>(MBS_LAUNCH_SIG); \
+    template hipError_t launch_skinny_xbf<a, b, c, d>(MBS_LAUNCH_SIG);
 #define MBS_GROUPED_INST(T) template hipError_t launch_bdirect_grouped<T>(MBS_LAUNCH_SIG);
 #define MBS_GROUPED_EXTERN(T) extern template hipError_t launch_bdirect_grouped<T>(MBS_LAUNCH_SIG);
 #define MBS_BDIRECT_EXTERN(T) extern template hipError_t launch_bdirect<T>(MBS_LAUNCH_SIG);
-#define MBS_SKINNY_EXTERN(a, b, c, d) extern template hipError_t launch_skinny<a, b, c, d>(MBS_LAUNCH_SIG);
+#define MBS_SKINNY_EXTERN(a, b, c, d)                                     \
+    extern template hipError_t launch_skinny<a, b, c, d>(MBS_LAUNCH_SIG); \
+    extern template hipError_t launch_skinny_xbf<a, b, c, d>(MBS_LAUNCH_SIG);
 
 }  // namespace mbs

@@ -393,21 +393,23 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
 __device__ __forceinline__ int floor_log2_bits(uint32_t u)
 {
     const int e = (int)((u >> 23) & 0xFF);
-    if (e != 0) return e - 127;
-    return (31 - __builtin_clz(u & 0x7FFFFFu)) - 149;
+    // (| 1 keeps clz defined for u == 0, whose result callers discard)
+    const int sub = (31 - __builtin_clz((u & 0x7FFFFFu) | 1u)) - 149;
+    return e != 0 ? e - 127 : sub;
 }
 
 // E8M0 scale of a block from its largest magnitude (fp32 bits, already times
 // the row multiplier m) and its NaN flag: floor(log2(amax)) - 2, biased by
 // 127 and clamped to [0, 254]; 0 for an all-zero block, 254 for an infinite
 // maximum, 255 (NaN) when the block holds a NaN.
+// (Selects, not early returns: the compiler keeps them branch-free.)
 __device__ __forceinline__ uint32_t e8m0_of(uint32_t amax_m, bool nan)
 {
-    if (nan) return 255;
-    if (amax_m == 0) return 0;
-    if (amax_m >= 0x7F800000u) return 254;
     const int e = floor_log2_bits(amax_m) - 2 + 127;
-    return (uint32_t)(e < 0 ? 0 : (e > 254 ? 254 : e));
+    uint32_t s = (uint32_t)(e < 0 ? 0 : (e > 254 ? 254 : e));
+    s = amax_m >= 0x7F800000u ? 254u : s;
+    s = amax_m == 0 ? 0u : s;
+    return nan ? 255u : s;
 }
 
 // 2^(s - 127) for s in [0, 254] as fp32: exponent field s, or the subnormal
@@ -415,6 +417,87 @@ __device__ __forceinline__ uint32_t e8m0_of(uint32_t amax_m, bool nan)
 __device__ __forceinline__ float e8m0_value(uint32_t s)
 {
     return s == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(s << 23);
+}
+
+// Largest 15-bit magnitude (bf16 bits without the sign) of eight bf16 values
+// (16 bytes); a NaN orders above inf.
+__device__ __forceinline__ uint32_t bf16x8_absmax(const i32x4 v)
+{
+    uint32_t mx = 0;
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t w = (uint32_t)v[i] & 0x7FFF7FFFu;
+        mx = max(mx, max(w & 0xFFFFu, w >> 16));
+    }
+    return mx;
+}
+
+// The same maximum over a whole 32-element block (four 16-byte pieces),
+// on both 16-bit halves at once (v_pk_max_u16), folded at the end.
+__device__ __forceinline__ uint32_t bf16x32_absmax(const i32x4 x[4])
+{
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 m = {0, 0};
+    for (int i = 0; i < 4; ++i) {
+        const i32x4 v = x[i];
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t w = (uint32_t)v[j] & 0x7FFF7FFFu;
+            m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w));
+        }
+    }
+    return max((uint32_t)m[0], (uint32_t)m[1]);
+}
+
+// Eight bf16 values -> one dword of packed e2m1 (element 2j in the low
+// nibble of byte j) under the block scale `sc`, with the gfx950 scaled
+// conversion v_cvt_scalef32_pk_fp4_bf16: code = RNE(v / sc) on the e2m1
+// grid, ties to the even code, saturating at 6, sign kept.  (Each word is
+// copied to a scalar first: hipcc's __builtin_bit_cast of a vector element
+// v[i] reads element 0.)
+__device__ __forceinline__ uint32_t bf16x8_to_e2m1(const i32x4 v, float sc)
+{
+    const uint32_t w0 = (uint32_t)v[0], w1 = (uint32_t)v[1], w2 = (uint32_t)v[2], w3 = (uint32_t)v[3];
+    // Each conversion writes one byte and keeps the other three; all four
+    // bytes are written below, so the starting value is w0 (dead after the
+    // first conversion) rather than a zero that costs a move.
+    uint32_t o = w0;
+    o = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(o, __builtin_bit_cast(bf16x2_t, w0), sc, 0);
+    o = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(o, __builtin_bit_cast(bf16x2_t, w1), sc, 1);
+    o = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(o, __builtin_bit_cast(bf16x2_t, w2), sc, 2);
+    o = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(o, __builtin_bit_cast(bf16x2_t, w3), sc, 3);
+    return o;
+}
+
+// One whole 32-element MXFP4 block in one lane: x[i] holds elements
+// 8i..8i+7 (bf16); returns the 16 packed bytes (dword i = elements 8i..8i+7)
+// and sets *s to the block's E8M0 byte.  Same rule and bytes as the
+// four-lanes-per-block quantizer kernel: a block holding a NaN gets scale
+// 255 and zero codes.
+__device__ __forceinline__ i32x4 quantize_block32(const i32x4 x[4], uint32_t* s)
+{
+    const uint32_t mx = bf16x32_absmax(x);
+    const bool nan = mx > 0x7F80u;
+    *s = e8m0_of(mx << 16, nan);
+    const float sc = e8m0_value(nan ? 127 : *s);
+    // The four dwords' conversion chains are interleaved (each chain writes
+    // one register byte by byte), and a NaN block is cleared with a mask:
+    // written as a select, the compiler branches around the conversions.
+    const uint32_t keep = nan ? 0u : ~0u;
+    uint32_t w[4][4], o[4];
+    for (int i = 0; i < 4; ++i) {
+        const i32x4 v = x[i];
+        w[i][0] = (uint32_t)v[0]; w[i][1] = (uint32_t)v[1];
+        w[i][2] = (uint32_t)v[2]; w[i][3] = (uint32_t)v[3];
+        o[i] = w[i][0];   // every byte is overwritten
+    }
+    static_for<4>([&](auto j) {
+        constexpr int J = decltype(j)::value;
+        for (int i = 0; i < 4; ++i)
+            o[i] = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(o[i], __builtin_bit_cast(bf16x2_t, w[i][J]), sc, J);
+    });
+    i32x4 q;
+    q[0] = (int)(o[0] & keep); q[1] = (int)(o[1] & keep);
+    q[2] = (int)(o[2] & keep); q[3] = (int)(o[3] & keep);
+    return q;
 }
 
 }  // namespace mbs

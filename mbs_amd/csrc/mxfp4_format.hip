@@ -59,24 +59,13 @@ quantize_bf16_kernel(const uint16_t* __restrict__ x, int rows, int K, uint8_t* _
     }
     const i32x4 v = *reinterpret_cast<const i32x4*>(x + (int64_t)r * K + (int64_t)j * 8);
     // magnitude maximum on the 15 magnitude bits: a NaN orders above inf
-    uint32_t mx = 0;
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t w = (uint32_t)v[i] & 0x7FFF7FFFu;
-        mx = max(mx, max(w & 0xFFFFu, w >> 16));
-    }
+    uint32_t mx = bf16x8_absmax(v);
     mx = max(mx, (uint32_t)__shfl_xor((int)mx, 1));
     mx = max(mx, (uint32_t)__shfl_xor((int)mx, 2));
     const bool nan = mx > 0x7F80u;
     const uint32_t s = e8m0_of(mx << 16, nan);
     const float sc = e8m0_value(nan ? 127 : s);
-    // (each word is copied to a scalar first: hipcc's __builtin_bit_cast of a
-    // vector element v[i] reads element 0)
-    const uint32_t w0 = (uint32_t)v[0], w1 = (uint32_t)v[1], w2 = (uint32_t)v[2], w3 = (uint32_t)v[3];
-    uint32_t o = 0;
-    o = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(o, __builtin_bit_cast(bf16x2_t, w0), sc, 0);
-    o = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(o, __builtin_bit_cast(bf16x2_t, w1), sc, 1);
-    o = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(o, __builtin_bit_cast(bf16x2_t, w2), sc, 2);
-    o = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(o, __builtin_bit_cast(bf16x2_t, w3), sc, 3);
+    const uint32_t o = bf16x8_to_e2m1(v, sc);
     *reinterpret_cast<uint32_t*>(packed + (int64_t)r * (K >> 1) + (int64_t)j * 4) = nan ? 0u : o;
     if ((threadIdx.x & 3) == 0) {
         const int b = j >> 2;

@@ -222,3 +222,61 @@ def test_grouped_whole_k_tiles_refuse_k_tails():
                                                    256, 256, K, 256, snp, 1.0, None, c, None)
             assert st == 4, (names[c], K)
             assert b"cannot run" in L.mbs_last_error()
+
+
+def from_bf16_lib():
+    L = c_lib()
+    P, I, S = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    L.mbs_gemm_a4w4_from_bf16_launch.argtypes = [I, I, P, P, P, P, I, I, I, I, I, ctypes.c_float,
+                                                 P, P, S, P]
+    L.mbs_gemm_a4w4_from_bf16_launch.restype = I
+    L.mbs_gemm_a4w4_from_bf16_workspace_bytes.argtypes = [I, I, I]
+    L.mbs_gemm_a4w4_from_bf16_workspace_bytes.restype = S
+    return L
+
+
+def test_from_bf16_entry_validates_before_launch():
+    """The bf16-activation decode entry: M > 32, a non-decode configuration,
+    a misaligned or null activation, a NaN alpha and bad shapes return their
+    status before any launch; M == 0 is a validated no-op."""
+    L = from_bf16_lib()
+    names = [L.mbs_gemm_a4w4_config_name(i).decode() for i in range(L.mbs_gemm_a4w4_num_configs())]
+    skinny = [i for i, n in enumerate(names) if n.startswith("skinny")]
+    other = [i for i, n in enumerate(names) if not n.startswith("skinny")]
+    assert len(skinny) == 7 and other
+    K, snp = 512, 16
+    go = lambda cfg, x, M, N=256, K=K, Mpad=None, snp=snp, alpha=1.0: L.mbs_gemm_a4w4_from_bf16_launch(
+        cfg, 0, x, FAKE, FAKE, FAKE, M, N, K, (M + 31) // 32 * 32 if Mpad is None else Mpad, snp,
+        alpha, None, None, 0, None)
+    assert go(-1, FAKE, 33) == 1 and b"M <= 32" in L.mbs_last_error()
+    assert go(-1, None, 4) == 1 and b"null" in L.mbs_last_error()
+    assert go(-1, FAKE + 8, 4) == 1 and b"aligned" in L.mbs_last_error()
+    assert go(-1, FAKE, 4, alpha=float("nan")) == 1
+    assert go(-1, FAKE, 4, N=250) == 1
+    assert go(-1, FAKE, 4, K=480, snp=16) == 1
+    assert go(-1, FAKE, 4, Mpad=64) == 1
+    for c in other:
+        assert go(c, FAKE, 4) == 4, names[c]
+        assert b"not a decode" in L.mbs_last_error()
+    assert go(len(names), FAKE, 4) == 4
+    # a 16-row decode config cannot take 17 rows
+    m16 = [i for i in skinny if "_m16_" in names[i]]
+    assert m16 and all(go(c, FAKE, 17) == 4 for c in m16)
+    assert go(-1, None, 0, Mpad=0) == 0   # empty batch: nothing launched
+    assert L.mbs_gemm_a4w4_from_bf16_workspace_bytes(33, 256, 512) == 0
+    assert L.mbs_gemm_a4w4_from_bf16_workspace_bytes(1, 8192, 8192) == 0   # no split at this size
+
+
+def test_from_bf16_plan_is_the_decode_plan():
+    """For decode shapes whose heuristic plan is a skinny one, the
+    bf16-activation entry's plan (skinny configurations only) is that same
+    plan, so both paths give the same bytes."""
+    L = from_bf16_lib()
+    buf = ctypes.create_string_buffer(256)
+    for M, N, K in [(1, 8192, 8192), (4, 8192, 8192), (16, 8192, 8192), (32, 8192, 8192),
+                    (8, 4096, 4096), (32, 2112, 7168), (1, 256, 512)]:
+        assert L.mbs_gemm_a4w4_plan_name(M, N, K, buf, 256) == 0
+        plan = buf.value.decode()
+        if plan.startswith("skinny"):
+            assert (L.mbs_gemm_a4w4_from_bf16_workspace_bytes(M, N, K)
+                    == L.mbs_gemm_a4w4_workspace_bytes(M, N, K)), (M, N, K, plan)
