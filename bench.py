@@ -262,7 +262,7 @@ def stream_floor(dev, nbytes=None, copies=10, replays=20, grids=(256, 512, 1024,
             "method": f"cold, {copies} rotating buffers, graph of {copies} launches replayed {replays}x"}
 
 
-def decode_bench(dev, Ms=(1, 4, 16, 32), N=8192, K=8192, copies=10, replays=20):
+def decode_bench(dev, Ms=(1, 4, 8, 16, 32), N=8192, K=8192, copies=10, replays=20):
     """Cold (rotating copies) and warm per-launch time of the decode shapes,
     from HIP-graph replay so host launch overhead is excluded.  Also, cold,
     the reference's decode flow from a bf16 activation: quantize_mxfp4, then

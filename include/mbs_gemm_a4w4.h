@@ -199,7 +199,7 @@ int mbs_gemm_a4w4_launch_config(int config, int splits, const uint8_t* A, const 
  * the two launches of the reference's decode flow, aiter's per_1x32 quantizer
  * then gemm_a4w4 (test_gemm_a4w4.py:134-141, bench_one.py:19-30); the
  * reference has no fused form.  Every workgroup quantizes the rows it needs
- * itself: for M <= 4 (only the live rows' blocks) this is faster than the two
+ * itself: for M <= 8 (only the live rows' blocks) this is faster than the two
  * launches; for larger M each workgroup re-quantizes 16 or 32 rows and the
  * two launches are faster (measured at N = K = 8192 on MI355X). */
 int mbs_gemm_a4w4_from_bf16_launch(int config, int splits, const void* x, const uint8_t* B,

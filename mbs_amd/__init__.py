@@ -83,7 +83,7 @@ def gemm_a4w4_from_bf16(x, B, B_scale, alpha: float = 1.0, bias=None, config: in
     flow, the per_1x32 quantizer then ``gemm_a4w4`` (test_gemm_a4w4.py:134-141,
     bench_one.py:19-30), with the same output bytes as quantizing x with
     ``quantize_mxfp4`` and calling ``gemm_a4w4`` on the result.  It runs in
-    one launch (the decode kernel quantizes x in registers) for M <= 4, where
+    one launch (the decode kernel quantizes x in registers) for M <= 8, where
     that is faster, and as the two launches otherwise; ``one_launch=True``
     forces the one-launch form (M <= 32), ``False`` the two launches.
     ``config``/``splits`` force a skinny (decode) configuration of the

@@ -423,13 +423,13 @@ at::Tensor gemm_a4w4_grouped(at::Tensor A, at::Tensor B, at::Tensor A_scale, at:
 // kernel quantizes x in registers, M <= 32) or two (quantize_mxfp4, then
 // gemm_a4w4).  Either way the bytes are those of quantize_mxfp4 followed by
 // gemm_a4w4 on the same plan.  one_launch: 1 forces the one-launch form, 0
-// the two launches, -1 picks the faster: one launch for M <= 4 (each
-// workgroup quantizes the live rows only: 7.6 / 8.3 us against 9.7 / 9.8 us
-// for two launches at M = 1 / 4, N = K = 8192, cold, MI355X), two launches
-// above (every workgroup re-quantizes all 16 or 32 rows of A: at M = 16 / 32
-// one launch takes longer than two).  config/splits force a skinny
-// configuration (one launch only; -1: the heuristic's).
-constexpr int64_t kOneLaunchMaxM = 4;
+// the two launches, -1 picks the faster: one launch for M <= 8 (each
+// workgroup quantizes the live rows only: 7.7 / 8.3 / 9.7 us against
+// 9.8 / 9.9 / 10.3 us for two launches at M = 1 / 4 / 8, N = K = 8192, cold,
+// MI355X), two launches above (every workgroup re-quantizes all 16 or 32
+// rows of A: at M = 16 / 32 one launch takes longer than two).  config/splits
+// force a skinny configuration (one launch only; -1: the heuristic's).
+constexpr int64_t kOneLaunchMaxM = 8;
 
 at::Tensor gemm_a4w4_from_bf16(at::Tensor x, at::Tensor B, at::Tensor B_scale, double alpha,
                                c10::optional<at::Tensor> bias, int64_t config, int64_t splits,
@@ -538,7 +538,7 @@ PYBIND11_MODULE(mbs_gemm_a4w4, m)
           [](int64_t c) { return std::string(mbs_gemm_a4w4_grouped_config_name((int)c)); });
     m.def("gemm_a4w4_from_bf16", &gemm_a4w4_from_bf16,
           "GEMM from a bf16 activation: quantize_mxfp4(x) then gemm_a4w4, in one launch "
-          "for M <= 4 (or when asked, M <= 32)",
+          "for M <= 8 (or when asked, M <= 32)",
           pybind11::arg("x"), pybind11::arg("B"), pybind11::arg("B_scale"),
           pybind11::arg("alpha") = 1.0, pybind11::arg("bias") = pybind11::none(),
           pybind11::arg("config") = -1, pybind11::arg("splits") = 0,

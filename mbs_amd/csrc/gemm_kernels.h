@@ -1489,10 +1489,11 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
 // scale layout would hold at the op_sel positions (row tile m, stage parity h
 // -> byte m + 2h).  The products equal quantizing A first and running the
 // XBF = 0 kernel on the same plan, bit for bit.  Every workgroup quantizes
-// all of A, so the quantizer's VALU work is repeated per workgroup; XBF = 2
-// (M <= 4, one row tile) quantizes only the live rows' blocks -- lane j takes
-// block (row j/16, stage (j/4)%4, K-block j%4) of a 4-stage batch -- and
-// moves codes and scale bytes to the MFMA lanes with ds_bpermute.
+// all of A, so the quantizer's VALU work is repeated per workgroup.  The
+// compact forms (one row tile) quantize only the live rows' blocks: XBF = 2
+// (M <= 4) in one pass, XBF = 3 (M <= 8) in two.  In pass q lane j takes
+// block (row 4q + j/16, stage (j/4)%4, K-block j%4) of a 4-stage batch;
+// ds_bpermute then moves codes and scale bytes to the MFMA lanes.
 template <int MT, int NF, int NWK, int U, bool SPLIT, int XBF = 0>
 __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
 {
@@ -1504,8 +1505,9 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
     // 4 fragments of A so nothing spills.  The accumulation order over the
     // stages does not depend on the batch.
     constexpr int UB = (XBF && NWK >= 8 && MT * U > 4) ? 4 / MT : U;
-    constexpr bool XC = XBF == 2;
-    static_assert(!XC || (MT == 1 && UB == 4), "compact bf16 A: one row tile, 4-stage batches");
+    constexpr bool XC = XBF >= 2;
+    constexpr int NP = XC ? XBF - 1 : 1;   // compact passes: 4 rows each
+    static_assert(!XC || (MT == 1 && UB == 4 && NP <= 2), "compact bf16 A: one row tile, 4-stage batches");
     __shared__ f32x4 red[NWK][NF * MT][64];
 
     const int lane = threadIdx.x & 63;
@@ -1547,15 +1549,17 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
         i32x4 b[UB][NF], a[UB][MT];
         int sb[UB / 2][NG], sa[UB / 2];
         i32x4 x[XBF == 1 ? UB : 1][XBF == 1 ? MT : 1][4];  // XBF 1: the lane's bf16 A blocks
-        i32x4 xc[4];                                        // XBF 2: block (lane/16, (lane/4)%4, lane%4)
+        i32x4 xc[NP][4];   // compact: block (row 4q + lane/16, stage (lane/4)%4, K-block lane%4)
         if constexpr (XC) {
             // first in the issue order: the quantization then waits for these
             // (from L2) and not for the batch's B stream; rows >= M lie
             // outside the range and read as zeros
             const int s = st + ((lane >> 2) & 3), kb = lane & 3;
             const bool zap = (ktail && s == S_total - 1 && kb >= 2) || s >= my_end;
-            const uint32_t o = (uint32_t)(((lane >> 4) * K + s * 128 + kb * 32) * 2);
-            static_for<4>([&](auto i) { xc[i] = load16(rA, zap ? kOOB : o + 16 * i); });
+            static_for<NP>([&](auto q) {
+                const uint32_t o = (uint32_t)(((4 * q + (lane >> 4)) * K + s * 128 + kb * 32) * 2);
+                static_for<4>([&](auto i) { xc[q][i] = load16(rA, zap ? kOOB : o + 16 * i); });
+            });
         }
         // Scales first: loads return in issue order, so stage u's MFMAs then
         // wait only for stage u's B and A, and the MFMAs trail the stream
@@ -1593,25 +1597,34 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
         // itself the scheduler interleaves them with the MFMAs and the wave
         // keeps only a fraction of its batch in flight.
         __builtin_amdgcn_sched_barrier(0);
-        i32x4 qc;
-        uint32_t qe = 0;
-        if constexpr (XC) qc = quantize_block32(xc, &qe);
+        i32x4 qc[NP];
+        uint32_t qe[NP] = {};
+        if constexpr (XC) static_for<NP>([&](auto q) { qc[q] = quantize_block32(xc[q], &qe[q]); });
         static_for<UB>([&](auto u) {
             constexpr int h = u & 1;
             const int s = st + u;
             const bool tail = ktail && s == S_total - 1 && hi_lane;
             int sav;
             if constexpr (XC) {
-                // MFMA lane (row l%16, K-block l/16) <- lane 16*row + 4u + l/16;
-                // rows 4..15 are past M
-                const bool live = (lane & 15) < 4;
-                const int src = (((lane & 15) * 16 + 4 * u + (lane >> 4)) & 63) * 4;
+                // MFMA lane (row r = l%16, K-block l/16) <- pass r/4, lane
+                // 16*(r%4) + 4u + l/16; rows from 4*NP on are past M
+                const int r = lane & 15;
+                const bool live = r < 4 * NP;
+                const int src = ((r & 3) * 16 + 4 * u + (lane >> 4)) * 4;
                 static_for<4>([&](auto i) {
                     constexpr int I = decltype(i)::value;
-                    const int v = __builtin_amdgcn_ds_bpermute(src, qc[I]);
+                    int v = __builtin_amdgcn_ds_bpermute(src, qc[0][I]);
+                    if constexpr (NP == 2) {
+                        const int v1 = __builtin_amdgcn_ds_bpermute(src, qc[1][I]);
+                        v = r >= 4 ? v1 : v;
+                    }
                     a[u][0][I] = live ? v : 0;
                 });
-                const uint32_t e = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)qe);
+                uint32_t e = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)qe[0]);
+                if constexpr (NP == 2) {
+                    const uint32_t e1 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)qe[1]);
+                    e = r >= 4 ? e1 : e;
+                }
                 sav = live ? (int)(e << (16 * h)) : 0;
             } else if constexpr (XBF) {
                 // this stage's blocks: codes into a[u][m], scales to byte m + 2h
@@ -1733,7 +1746,7 @@ hipError_t launch_skinny(const GemmArgs& a, dim3 grid, bool, bool split, hipStre
 }
 
 // The same plans with A given as bf16 and quantized in registers; one row
-// tile with M <= 4 takes the compact form.
+// tile with M <= 8 takes a compact form.
 template <int MT, int NF, int NWK, int U>
 hipError_t launch_skinny_xbf(const GemmArgs& a, dim3 grid, bool, bool split, hipStream_t s)
 {
@@ -1741,6 +1754,11 @@ hipError_t launch_skinny_xbf(const GemmArgs& a, dim3 grid, bool, bool split, hip
         if (a.M <= 4) {
             if (split) hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, true, 2>), grid, dim3(64 * NWK), 0, s, a);
             else hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, false, 2>), grid, dim3(64 * NWK), 0, s, a);
+            return hipGetLastError();
+        }
+        if (a.M <= 8) {
+            if (split) hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, true, 3>), grid, dim3(64 * NWK), 0, s, a);
+            else hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, false, 3>), grid, dim3(64 * NWK), 0, s, a);
             return hipGetLastError();
         }
     }

@@ -59,9 +59,9 @@ def same_bits(got, want, tag):
     assert torch.equal(got.view(torch.int16), want.view(torch.int16)), tag
 
 
-@pytest.mark.parametrize("M", [1, 4, 16, 32])
+@pytest.mark.parametrize("M", [1, 4, 8, 16, 32])
 def test_decode_shapes_default_plan(dev, M):
-    """configs[2] shapes: one launch equals quantize + gemm_a4w4."""
+    """configs[2] shapes (and M = 8): one launch equals quantize + gemm_a4w4."""
     import mbs_amd
 
     N = K = 8192
@@ -78,6 +78,7 @@ def test_decode_shapes_default_plan(dev, M):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 256, 512), (3, 1280, 576), (2, 4096, 4160),
+                                   (8, 1280, 576), (6, 96, 64),
                                    (17, 2112, 7168), (32, 1280, 576),
                                    (5, 4096, 4160), (32, 48, 64)])
 def test_every_decode_config_and_split(dev, M, N, K):
