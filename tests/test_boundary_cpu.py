@@ -280,3 +280,28 @@ def test_from_bf16_plan_is_the_decode_plan():
         if plan.startswith("skinny"):
             assert (L.mbs_gemm_a4w4_from_bf16_workspace_bytes(M, N, K)
                     == L.mbs_gemm_a4w4_workspace_bytes(M, N, K)), (M, N, K, plan)
+
+
+@pytest.mark.parametrize("passes", [1, 2])
+def test_compact_bf16_lane_map_is_a_bijection(passes):
+    """The compact one-launch decode form (gemm_skinny_kernel, XBF = 2/3):
+    in pass q lane j quantizes block (row 4q + j/16, stage (j/4)%4, K-block
+    j%4) of a 4-stage batch, and MFMA lane l of stage u reads pass (l%16)/4,
+    lane 16*((l%16)%4) + 4u + l/16.  Every MFMA lane of a live row must read
+    exactly the block its operand layout wants (row l%16, K-block l/16), and
+    every quantized block is read exactly once."""
+    produced = {}
+    for q in range(passes):
+        for j in range(64):
+            produced[(q, j)] = (4 * q + j // 16, (j // 4) % 4, j % 4)   # (row, stage, kblock)
+    seen = []
+    for u in range(4):
+        for lane in range(64):
+            r = lane % 16
+            if r >= 4 * passes:
+                continue   # rows past the compact form's reach read zeros
+            src = (r % 4) * 16 + 4 * u + lane // 16
+            got = produced[(r // 4, src)]
+            assert got == (r, u, lane // 16), (passes, u, lane, got)
+            seen.append(got)
+    assert sorted(seen) == sorted(produced.values())
