@@ -268,7 +268,8 @@ def decode_bench(dev, Ms=(1, 4, 8, 16, 32), N=8192, K=8192, copies=10, replays=2
     the reference's decode flow from a bf16 activation: quantize_mxfp4, then
     gemm_a4w4 (two launches), and the same product in one launch
     (gemm_a4w4_from_bf16(one_launch=True): the decode kernel quantizes in
-    registers)."""
+    registers); for M <= 8 also both with MBS activations (quantize_mxfp4_mbs
+    and the factor GEMM, against the one-launch MBS form)."""
     import torch
 
     import mbs_amd
@@ -277,21 +278,34 @@ def decode_bench(dev, Ms=(1, 4, 8, 16, 32), N=8192, K=8192, copies=10, replays=2
         a, s = mbs_amd.quantize_mxfp4(x, shuffle=True)
         return mbs_amd.gemm_a4w4(a, B, s, Bs)
 
+    def two_step_mbs(x, B, Bs, Bf):
+        a, s, f = mbs_amd.quantize_mxfp4_mbs(x, shuffle=True)
+        return mbs_amd.gemm_a4w4(a, B, s, Bs, f, Bf)
+
     (_, B, _, Bs), _ = prepare(32, N, K, 2, dev)
     Bc = [B.clone() for _ in range(copies)]
     Bsc = [Bs.clone() for _ in range(copies)]
+    Bf = torch.randint(0, 256, (N,), dtype=torch.uint8, generator=torch.Generator().manual_seed(7)).to(dev)
     del B, Bs
     res = {}
     for M in Ms:
         (A, _, As, _), (xh, _) = prepare(M, 16, K, 2, dev)
         x = xh.to(dev)
-        for mode in ("cold", "warm", "quantize+gemm", "one_launch"):
+        modes = ["cold", "warm", "quantize+gemm", "one_launch"]
+        if M <= 8:   # MBS activations (the one-launch MBS form takes M <= 8)
+            modes += ["quantize_mbs+gemm", "one_launch_mbs"]
+        for mode in modes:
             idx = [0] * copies if mode == "warm" else list(range(copies))
             if mode == "quantize+gemm":
                 run = lambda: [two_step(x, Bc[i], Bsc[i]) for i in idx]
             elif mode == "one_launch":
                 run = lambda: [mbs_amd.gemm_a4w4_from_bf16(x, Bc[i], Bsc[i], one_launch=True)
                                for i in idx]
+            elif mode == "quantize_mbs+gemm":
+                run = lambda: [two_step_mbs(x, Bc[i], Bsc[i], Bf) for i in idx]
+            elif mode == "one_launch_mbs":
+                run = lambda: [mbs_amd.gemm_a4w4_from_bf16(x, Bc[i], Bsc[i], B_factor=Bf,
+                                                           one_launch=True) for i in idx]
             else:
                 run = lambda: [mbs_amd.gemm_a4w4(A, Bc[i], As, Bsc[i]) for i in idx]
             run()
@@ -309,7 +323,7 @@ def decode_bench(dev, Ms=(1, 4, 8, 16, 32), N=8192, K=8192, copies=10, replays=2
             torch.cuda.synchronize()
             us = e0.elapsed_time(e1) * 1e3 / (replays * copies)
             gbs = algo_bytes(M, N, K) / (us * 1e-6) / 1e9
-            if mode in ("quantize+gemm", "one_launch"):
+            if mode not in ("cold", "warm"):
                 res.setdefault(f"M={M}", {})[f"cold_{mode}_us"] = round(us, 3)
             else:
                 res.setdefault(f"M={M}", {})[mode] = {

@@ -189,7 +189,14 @@ int mbs_gemm_a4w4_launch_config(int config, int splits, const uint8_t* A, const 
  * is written back) and multiplied by B as in mbs_gemm_a4w4_launch_ex with no
  * factors:  out[m][n] = bf16(C[m][n] * alpha + bias[n]).  The output bytes
  * equal mbs_quantize_mxfp4_bf16 (shuffled scales) followed by
- * mbs_gemm_a4w4_launch_ex on the same decode plan: config < 0 takes the
+ * mbs_gemm_a4w4_launch_ex on the same decode plan.  With BFactor ([N] u8, or
+ * NULL) the activation is MBS-quantized instead (the rule of
+ * mbs_quantize_mxfp4_mbs_bf16: each row's factor byte from its maximum over
+ * all of K, derived inside the kernel) and the factor epilogue applies both
+ * factors; the bytes equal mbs_quantize_mxfp4_mbs_bf16 followed by
+ * mbs_gemm_a4w4_launch_ex with AFactor and BFactor.  MBS takes M <= 8 and a
+ * 16-row decode configuration without K splits (MBS_ERR_ARGUMENT /
+ * MBS_ERR_CONFIG otherwise) and no workspace.  config < 0 takes the
  * plan the heuristic picks among the skinny (decode) configurations, the
  * one mbs_gemm_a4w4_launch runs for these shapes; config >= 0 must name a
  * skinny configuration (MBS_ERR_CONFIG otherwise), with `splits` as in
@@ -203,9 +210,10 @@ int mbs_gemm_a4w4_launch_config(int config, int splits, const uint8_t* A, const 
  * launches; for larger M each workgroup re-quantizes 16 or 32 rows and the
  * two launches are faster (measured at N = K = 8192 on MI355X). */
 int mbs_gemm_a4w4_from_bf16_launch(int config, int splits, const void* x, const uint8_t* B,
-                                   const uint8_t* BScale, void* out, int M, int N, int K,
-                                   int Mpad, int scaleN_pad, float alpha, const void* bias,
-                                   void* workspace, size_t workspace_bytes, void* stream);
+                                   const uint8_t* BScale, const uint8_t* BFactor, void* out, int M,
+                                   int N, int K, int Mpad, int scaleN_pad, float alpha,
+                                   const void* bias, void* workspace, size_t workspace_bytes,
+                                   void* stream);
 /* Workspace the heuristic (config < 0) bf16-activation launch wants. */
 size_t mbs_gemm_a4w4_from_bf16_workspace_bytes(int M, int N, int K);
 

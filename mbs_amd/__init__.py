@@ -78,7 +78,7 @@ def gemm_a4w4(A, B, A_scale, B_scale, A_factor=None, B_factor=None, alpha: float
 
 
 def gemm_a4w4_from_bf16(x, B, B_scale, alpha: float = 1.0, bias=None, config: int = -1,
-                        splits: int = 0, one_launch=None):
+                        splits: int = 0, one_launch=None, B_factor=None):
     """out[M,N] bf16 from a bf16 activation x [M,K]: the reference's decode
     flow, the per_1x32 quantizer then ``gemm_a4w4`` (test_gemm_a4w4.py:134-141,
     bench_one.py:19-30), with the same output bytes as quantizing x with
@@ -87,9 +87,12 @@ def gemm_a4w4_from_bf16(x, B, B_scale, alpha: float = 1.0, bias=None, config: in
     that is faster, and as the two launches otherwise; ``one_launch=True``
     forces the one-launch form (M <= 32), ``False`` the two launches.
     ``config``/``splits`` force a skinny (decode) configuration of the
-    one-launch form."""
+    one-launch form.  With ``B_factor`` (the weights' MBS factor bytes) x is
+    MBS-quantized instead, as ``quantize_mxfp4_mbs`` does, and both factors
+    apply (one launch by default for M <= 4, forced up to M <= 8: the row
+    factors are derived in the kernel)."""
     mode = -1 if one_launch is None else int(bool(one_launch))
-    return ext().gemm_a4w4_from_bf16(x, B, B_scale, alpha, bias, config, splits, mode)
+    return ext().gemm_a4w4_from_bf16(x, B, B_scale, B_factor, alpha, bias, config, splits, mode)
 
 
 def gemm_a4w4_grouped(A, B, A_scale, B_scale, group_offsets, A_factor=None, B_factor=None,

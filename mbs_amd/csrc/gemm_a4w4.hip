@@ -358,12 +358,15 @@ int config_index(const char* name)
 
 // skinny_only: choose among the decode (skinny) configurations only; for a
 // shape whose unrestricted choice is skinny this is the same plan.
-bool choose_plan(int M, int N, int K, size_t ws_avail, Plan* best, bool skinny_only = false)
+// max_bm: only configurations covering at most that many rows per tile.
+bool choose_plan(int M, int N, int K, size_t ws_avail, Plan* best, bool skinny_only = false,
+                 int max_bm = 1 << 30)
 {
     for (const TunedPlan& t : kTuned) {
         if (t.M != M || t.N != N || t.K != K) continue;
         const int c = config_index(t.config);
         if (skinny_only && (c < 0 || kConfigs[c].family != kSkinny)) continue;
+        if (c >= 0 && kConfigs[c].bm > max_bm) continue;
         Plan pl;
         if (c >= 0 && make_plan(c, t.splits, M, N, K, &pl) && pl.ws_bytes <= ws_avail) {
             *best = pl;
@@ -374,7 +377,7 @@ bool choose_plan(int M, int N, int K, size_t ws_avail, Plan* best, bool skinny_o
     double best_cost = 0;
     for (int i = 0; i < kNumConfigs; ++i) {
         const bool skinny = kConfigs[i].family == kSkinny;
-        if (skinny_only && !skinny) continue;
+        if ((skinny_only && !skinny) || kConfigs[i].bm > max_bm) continue;
         for (int want : {0, 1, 2, 4, 8}) {
             if (skinny != (want == 0)) continue;  // skinny: its own split rule
             Plan pl;
@@ -436,13 +439,17 @@ int validate(const uint8_t* A, const uint8_t* B, const uint8_t* As, const uint8_
 }
 
 // Arguments of the bf16-activation entry: x (bf16 [M, K]) takes the place
-// of A and its scales; decode shapes only.
-int validate_from_bf16(const void* x, const uint8_t* B, const uint8_t* Bs, void* out, int M,
-                       int N, int K, int Mpad, int snp)
+// of A and its scales; decode shapes only (M <= 8 with MBS factors).
+int validate_from_bf16(const void* x, const uint8_t* B, const uint8_t* Bs, const uint8_t* Bf,
+                       void* out, int M, int N, int K, int Mpad, int snp)
 {
     if (M > 32)
         return fail(MBS_ERR_ARGUMENT, "the bf16-activation GEMM takes M <= 32 (decode shapes), got M=" +
                                           std::to_string(M));
+    if (Bf && M > 8)
+        return fail(MBS_ERR_ARGUMENT, "the bf16-activation GEMM with MBS factors takes M <= 8, got M=" +
+                                          std::to_string(M));
+    if (misaligned(Bf, 4)) return fail(MBS_ERR_ARGUMENT, "BFactor must be 4-byte aligned");
     if (M > 0 && !x) return fail(MBS_ERR_ARGUMENT, "null activation pointer");
     if (misaligned(x, 16)) return fail(MBS_ERR_ARGUMENT, "x must be 16-byte aligned");
     // The remaining checks are the packed entry's (x stands in for A and its
@@ -809,28 +816,36 @@ size_t mbs_gemm_a4w4_from_bf16_workspace_bytes(int M, int N, int K)
 }
 
 int mbs_gemm_a4w4_from_bf16_launch(int config, int splits, const void* x, const uint8_t* B,
-                                   const uint8_t* BScale, void* out, int M, int N, int K,
-                                   int Mpad, int scaleN_pad, float alpha, const void* bias,
-                                   void* workspace, size_t workspace_bytes, void* stream)
+                                   const uint8_t* BScale, const uint8_t* BFactor, void* out, int M,
+                                   int N, int K, int Mpad, int scaleN_pad, float alpha,
+                                   const void* bias, void* workspace, size_t workspace_bytes,
+                                   void* stream)
 {
     set_last_error("");
-    int st = validate_from_bf16(x, B, BScale, out, M, N, K, Mpad, scaleN_pad);
+    int st = validate_from_bf16(x, B, BScale, BFactor, out, M, N, K, Mpad, scaleN_pad);
     if (st != MBS_OK) return st;
     if (!(alpha == alpha)) return fail(MBS_ERR_ARGUMENT, "alpha is NaN");
     if (config >= kNumConfigs || (config >= 0 && kConfigs[config].family != kSkinny))
         return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) +
                                         " is not a decode (skinny) configuration");
+    // MBS: one 16-row tile (the compact forms) and no K split, since every
+    // workgroup derives the row factors from the whole row
+    const bool mbs = BFactor != nullptr;
+    if (mbs && config >= 0 && (kConfigs[config].bm != 16 || splits > 1))
+        return fail(MBS_ERR_CONFIG, "with MBS factors the config must be a 16-row decode "
+                                    "configuration without K splits");
     if (M == 0) return MBS_OK;
     Plan pl;
     if (config < 0) {
-        if (!choose_plan(M, N, K, workspace ? workspace_bytes : 0, &pl, true))
+        if (!choose_plan(M, N, K, mbs ? 0 : (workspace ? workspace_bytes : 0), &pl, true,
+                         mbs ? 16 : 1 << 30))
             return fail(MBS_ERR_CONFIG, "no decode configuration fits this problem");
-    } else if (!make_plan(config, splits, M, N, K, &pl)) {
+    } else if (!make_plan(config, mbs ? 1 : splits, M, N, K, &pl)) {
         return fail(MBS_ERR_CONFIG, "config " + std::to_string(config) + " cannot run M=" +
                                         std::to_string(M) + " K=" + std::to_string(K) + " with " +
                                         std::to_string(splits) + " splits");
     }
-    return run_plan(pl, static_cast<const uint8_t*>(x), B, nullptr, BScale, nullptr, nullptr, out,
+    return run_plan(pl, static_cast<const uint8_t*>(x), B, nullptr, BScale, nullptr, BFactor, out,
                     M, N, K, scaleN_pad, workspace, workspace_bytes, stream, alpha, bias, true);
 }
 

@@ -429,19 +429,36 @@ at::Tensor gemm_a4w4_grouped(at::Tensor A, at::Tensor B, at::Tensor A_scale, at:
 // MI355X), two launches above (every workgroup re-quantizes all 16 or 32
 // rows of A: at M = 16 / 32 one launch takes longer than two).  config/splits
 // force a skinny configuration (one launch only; -1: the heuristic's).
+// With MBS activations every workgroup first takes the rows' maxima over all
+// of K: one launch for M <= 4 (9.8 / 10.6 us against 11.4 / 11.8 us for
+// quantize_mxfp4_mbs + the factor GEMM at M = 1 / 4), two launches above
+// (14.4 against 12.0 us at M = 8).
 constexpr int64_t kOneLaunchMaxM = 8;
+constexpr int64_t kOneLaunchMaxMbsM = 4;
 
-at::Tensor gemm_a4w4_from_bf16(at::Tensor x, at::Tensor B, at::Tensor B_scale, double alpha,
+// With B_factor the activation is MBS-quantized (quantize_mxfp4_mbs, its
+// factor bytes derived in the kernel in the one-launch form, M <= 8).
+at::Tensor gemm_a4w4_from_bf16(at::Tensor x, at::Tensor B, at::Tensor B_scale,
+                               c10::optional<at::Tensor> B_factor, double alpha,
                                c10::optional<at::Tensor> bias, int64_t config, int64_t splits,
                                int64_t one_launch)
 {
     TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.scalar_type() == at::kBFloat16,
                 "gemm_a4w4_from_bf16: x must be a 2D bf16 device tensor");
-    const bool one = one_launch > 0 || config >= 0 || (one_launch < 0 && x.size(0) <= kOneLaunchMaxM);
-    TORCH_CHECK(!(one && x.size(0) > 32), "gemm_a4w4_from_bf16: the one-launch form needs M <= 32");
+    const bool mbs = B_factor.has_value() && B_factor->defined();
+    const int64_t max_one = mbs ? 8 : 32;
+    const bool one = one_launch > 0 || config >= 0 ||
+                     (one_launch < 0 && x.size(0) <= (mbs ? kOneLaunchMaxMbsM : kOneLaunchMaxM));
+    TORCH_CHECK(!(one && x.size(0) > max_one), "gemm_a4w4_from_bf16: the one-launch form needs M <= ",
+                max_one, mbs ? " with MBS factors" : "");
     TORCH_CHECK(!(one_launch == 0 && config >= 0),
                 "gemm_a4w4_from_bf16: a forced config runs the one-launch form");
     if (!one) {
+        if (mbs) {
+            auto q = quantize_mxfp4_mbs(x, true, 127);
+            return run(prepare(std::get<0>(q), B, std::get<1>(q), B_scale, std::get<2>(q), B_factor),
+                       -1, 0, alpha, bias);
+        }
         auto q = quantize_mxfp4(x, true, 127);
         return run(prepare(std::get<0>(q), B, std::get<1>(q), B_scale, c10::nullopt, c10::nullopt),
                    -1, 0, alpha, bias);
@@ -462,21 +479,29 @@ at::Tensor gemm_a4w4_from_bf16(at::Tensor x, at::Tensor B, at::Tensor B_scale, d
     c10::DeviceGuard guard(x.device());
     const int64_t Mpad = round_up(M, 32);
     auto out = torch::empty({Mpad, N}, torch::TensorOptions().dtype(torch::kBFloat16).device(x.device()));
-    const size_t ws = config < 0 ? mbs_gemm_a4w4_from_bf16_workspace_bytes((int)M, (int)N, (int)K)
-                                 : mbs_gemm_a4w4_config_workspace_bytes((int)config, (int)splits,
-                                                                        (int)M, (int)N, (int)K);
+    // (MBS launches use no K split and so no workspace)
+    const size_t ws = mbs ? 0
+                      : config < 0 ? mbs_gemm_a4w4_from_bf16_workspace_bytes((int)M, (int)N, (int)K)
+                                   : mbs_gemm_a4w4_config_workspace_bytes((int)config, (int)splits,
+                                                                          (int)M, (int)N, (int)K);
     at::Tensor wst;
     if (ws) wst = torch::empty({(int64_t)ws}, torch::TensorOptions().dtype(torch::kByte).device(x.device()));
-    at::Tensor bu;
+    at::Tensor bu, bf;
     if (bias.has_value()) {
         TORCH_CHECK(bias->is_cuda() && bias->device() == x.device() &&
                         bias->scalar_type() == at::kBFloat16 && bias->numel() == N,
                     "gemm_a4w4_from_bf16: bias must be a bf16 device tensor of N entries");
         bu = aligned_contiguous(*bias);
     }
+    if (mbs) {
+        bf = as_bytes(*B_factor, 4);
+        TORCH_CHECK(bf.is_cuda() && bf.device() == x.device() && bf.numel() == N,
+                    "gemm_a4w4_from_bf16: B_factor must hold N = ", N, " bytes on the device");
+    }
     check_status(mbs_gemm_a4w4_from_bf16_launch(
                      (int)config, (int)splits, xc.data_ptr(), Bb.data_ptr<uint8_t>(),
-                     Bsb.data_ptr<uint8_t>(), out.data_ptr(), (int)M, (int)N, (int)K, (int)Mpad,
+                     Bsb.data_ptr<uint8_t>(), mbs ? bf.data_ptr<uint8_t>() : nullptr,
+                     out.data_ptr(), (int)M, (int)N, (int)K, (int)Mpad,
                      (int)scale_pad(K), (float)alpha, bu.defined() ? bu.data_ptr() : nullptr,
                      ws ? wst.data_ptr() : nullptr, ws, current_stream(x)),
                  "gemm_a4w4_from_bf16");
@@ -540,9 +565,9 @@ PYBIND11_MODULE(mbs_gemm_a4w4, m)
           "GEMM from a bf16 activation: quantize_mxfp4(x) then gemm_a4w4, in one launch "
           "for M <= 8 (or when asked, M <= 32)",
           pybind11::arg("x"), pybind11::arg("B"), pybind11::arg("B_scale"),
-          pybind11::arg("alpha") = 1.0, pybind11::arg("bias") = pybind11::none(),
-          pybind11::arg("config") = -1, pybind11::arg("splits") = 0,
-          pybind11::arg("one_launch") = -1);
+          pybind11::arg("B_factor") = pybind11::none(), pybind11::arg("alpha") = 1.0,
+          pybind11::arg("bias") = pybind11::none(), pybind11::arg("config") = -1,
+          pybind11::arg("splits") = 0, pybind11::arg("one_launch") = -1);
     m.def("plan_name", &plan_name, "kernel plan the heuristic picks for (M, N, K)");
     m.def("num_configs", []() { return mbs_gemm_a4w4_num_configs(); });
     m.def("config_name", [](int64_t c) { return std::string(mbs_gemm_a4w4_config_name((int)c)); });

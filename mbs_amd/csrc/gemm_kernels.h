@@ -1494,7 +1494,12 @@ __global__ void __launch_bounds__(T::NT) gemm_bdirect_kernel(const GemmArgs p)
 // (M <= 4) in one pass, XBF = 3 (M <= 8) in two.  In pass q lane j takes
 // block (row 4q + j/16, stage (j/4)%4, K-block j%4) of a 4-stage batch;
 // ds_bpermute then moves codes and scale bytes to the MFMA lanes.
-template <int MT, int NF, int NWK, int U, bool SPLIT, int XBF = 0>
+// XMBS (compact forms, no K split): MBS activations.  Every workgroup first
+// takes each row's maximum over all of K (its waves split K, then reduce
+// through LDS), derives the row's factor byte as the MBS quantizer does, and
+// quantizes the row times 1 + b/256; the epilogue applies f(b) with the B
+// factors (p.Bf) as the factor GEMM does with a stored A factor.
+template <int MT, int NF, int NWK, int U, bool SPLIT, int XBF = 0, bool XMBS = false>
 __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
 {
     static_assert(U % 2 == 0, "batch must cover whole 256-K scale groups");
@@ -1508,7 +1513,10 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
     constexpr bool XC = XBF >= 2;
     constexpr int NP = XC ? XBF - 1 : 1;   // compact passes: 4 rows each
     static_assert(!XC || (MT == 1 && UB == 4 && NP <= 2), "compact bf16 A: one row tile, 4-stage batches");
+    static_assert(!XMBS || (XC && !SPLIT), "MBS activations: compact forms, whole K");
     __shared__ f32x4 red[NWK][NF * MT][64];
+    __shared__ uint32_t row_max[XMBS ? NWK : 1][8];
+    __shared__ uint32_t row_fb[16];   // rows 8..15 (past M) stay 0
 
     const int lane = threadIdx.x & 63;
     const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1544,6 +1552,28 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
     static_for<NF>([&](auto f) {
         static_for<MT>([&](auto m) { acc[f][m] = f32x4{0.f, 0.f, 0.f, 0.f}; });
     });
+
+    float mrow[NP];   // XMBS: the multiplier 1 + b/256 of each pass's row
+    if constexpr (XMBS) {
+        for (int r = 0; r < 4 * NP; ++r) {   // rows >= M read zeros
+            uint32_t amax = 0;
+            for (int e = (kw * 64 + lane) * 8; e < K; e += NWK * 64 * 8)
+                amax = max(amax, bf16x8_absmax(load16(rA, (uint32_t)((r * K + e) * 2))));
+            for (int off = 32; off >= 1; off >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, off));
+            if (lane == 0) row_max[kw][r] = amax;
+        }
+        __syncthreads();
+        if (threadIdx.x < 16) {
+            uint32_t amax = 0;
+            if (threadIdx.x < 4 * NP)
+                for (int k = 0; k < NWK; ++k) amax = max(amax, row_max[k][threadIdx.x]);
+            row_fb[threadIdx.x] = mbs_factor_byte(amax);
+        }
+        __syncthreads();
+        static_for<NP>([&](auto q) {
+            mrow[q] = __uint_as_float(0x3F800000u | (row_fb[4 * q + (lane >> 4)] << 15));
+        });
+    }
 
     for (int st = my_begin; st < my_end; st += UB) {
         i32x4 b[UB][NF], a[UB][MT];
@@ -1599,7 +1629,8 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
         __builtin_amdgcn_sched_barrier(0);
         i32x4 qc[NP];
         uint32_t qe[NP] = {};
-        if constexpr (XC) static_for<NP>([&](auto q) { qc[q] = quantize_block32(xc[q], &qe[q]); });
+        if constexpr (XMBS) static_for<NP>([&](auto q) { qc[q] = quantize_block32_mbs(xc[q], mrow[q], &qe[q]); });
+        else if constexpr (XC) static_for<NP>([&](auto q) { qc[q] = quantize_block32(xc[q], &qe[q]); });
         static_for<UB>([&](auto u) {
             constexpr int h = u & 1;
             const int s = st + u;
@@ -1670,10 +1701,11 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
             const rsrc_t rW = make_rsrc(p.ws + (size_t)split * p.M * p.N, (uint32_t)(p.M * p.N * 4));
             store16(rW, (uint32_t)((row * p.N + c) * 4), v);
         } else {
-            if (p.Af && p.Bf) {
-                const rsrc_t rAf = make_rsrc(p.Af, (uint32_t)p.M);
+            if (XMBS || (p.Af && p.Bf)) {
+                const rsrc_t rAf = make_rsrc(p.Af, XMBS ? 0u : (uint32_t)p.M);
                 const rsrc_t rBf = make_rsrc(p.Bf, (uint32_t)p.N);
-                const float fa = factor_of(load1(rAf, row)) * p.alpha;
+                const uint32_t ab = XMBS ? row_fb[row] : load1(rAf, row);
+                const float fa = factor_of(ab) * p.alpha;
                 const uint32_t bytes = (uint32_t)load4(rBf, c);
                 for (int q = 0; q < 4; ++q) v[q] = v[q] * (fa * factor_of(bytes >> (8 * q)));
             } else if (p.alpha != 1.0f) {
@@ -1751,6 +1783,14 @@ template <int MT, int NF, int NWK, int U>
 hipError_t launch_skinny_xbf(const GemmArgs& a, dim3 grid, bool, bool split, hipStream_t s)
 {
     if constexpr (MT == 1) {
+        // MBS activations (B factors given, the A factors derived in the
+        // kernel): compact forms without a K split only
+        if (a.Bf) {
+            if (split || a.M > 8) return hipErrorInvalidValue;
+            if (a.M <= 4) hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, false, 2, true>), grid, dim3(64 * NWK), 0, s, a);
+            else hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, false, 3, true>), grid, dim3(64 * NWK), 0, s, a);
+            return hipGetLastError();
+        }
         if (a.M <= 4) {
             if (split) hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, true, 2>), grid, dim3(64 * NWK), 0, s, a);
             else hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, false, 2>), grid, dim3(64 * NWK), 0, s, a);
@@ -1762,6 +1802,7 @@ hipError_t launch_skinny_xbf(const GemmArgs& a, dim3 grid, bool, bool split, hip
             return hipGetLastError();
         }
     }
+    if (a.Bf) return hipErrorInvalidValue;
     if (split) hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, true, 1>), grid, dim3(64 * NWK), 0, s, a);
     else hipLaunchKernelGGL((gemm_skinny_kernel<MT, NF, NWK, U, false, 1>), grid, dim3(64 * NWK), 0, s, a);
     return hipGetLastError();

@@ -500,4 +500,41 @@ __device__ __forceinline__ i32x4 quantize_block32(const i32x4 x[4], uint32_t* s)
     return q;
 }
 
+// One whole block of an MBS-scaled row in one lane: the block's elements
+// times the row multiplier m = 1 + b/256 (fp32 products), quantized with the
+// rule and conversion of the MBS quantizer kernel (block maximum of the bf16
+// magnitudes times m for the scale, v_cvt_scalef32_pk_fp4_f32 of the scaled
+// values); a block holding a NaN gets scale 255 and zero codes.
+__device__ __forceinline__ i32x4 quantize_block32_mbs(const i32x4 x[4], float m, uint32_t* s)
+{
+    const uint32_t mx = bf16x32_absmax(x);
+    const bool nan = mx > 0x7F80u;
+    *s = e8m0_of(__float_as_uint(__uint_as_float(mx << 16) * m), nan);
+    const float sc = e8m0_value(nan ? 127 : *s);
+    const uint32_t keep = nan ? 0u : ~0u;
+    i32x4 q;
+    for (int i = 0; i < 4; ++i) {
+        const i32x4 v = x[i];
+        const uint32_t w[4] = {(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+        uint32_t o = w[0];   // every byte is overwritten
+        static_for<4>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            const float lo = __uint_as_float(w[j] << 16) * m;
+            const float hi = __uint_as_float(w[j] & 0xFFFF0000u) * m;
+            o = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(o, lo, hi, sc, j);
+        });
+        q[i] = (int)(o & keep);
+    }
+    return q;
+}
+
+// MBS factor byte of a row from its largest bf16 magnitude (15 bits): the top
+// 8 mantissa bits of 6/max (IEEE division, then truncation); 0 for a zero,
+// infinite or NaN maximum.  The row is quantized times 1 + b/256.
+__device__ __forceinline__ uint32_t mbs_factor_byte(uint32_t amax)
+{
+    if (amax == 0 || amax >= 0x7F80) return 0;
+    return (__float_as_uint(__fdiv_rn(6.0f, __uint_as_float(amax << 16))) >> 15) & 0xFF;
+}
+
 }  // namespace mbs

@@ -124,11 +124,7 @@ quantize_mbs_bf16_kernel(const uint16_t* __restrict__ x, int rows, int K, uint8_
     __syncthreads();
     amax = red[0];
     for (int i = 1; i < 4; ++i) amax = red[i] > amax ? red[i] : amax;
-    uint32_t fb = 0;
-    if (amax != 0 && amax < 0x7F80) {  // finite, non-zero
-        const float q = __fdiv_rn(6.0f, __uint_as_float(amax << 16));
-        fb = (__float_as_uint(q) >> 15) & 0xFF;
-    }
+    const uint32_t fb = mbs_factor_byte(amax);
     const float m = __uint_as_float(0x3F800000u | (fb << 15));
     if (threadIdx.x == 0) factors[r] = (uint8_t)fb;
     // Quantize pass, four lanes per 32-element block as in the plain kernel:

@@ -227,8 +227,8 @@ def test_grouped_whole_k_tiles_refuse_k_tails():
 def from_bf16_lib():
     L = c_lib()
     P, I, S = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
-    L.mbs_gemm_a4w4_from_bf16_launch.argtypes = [I, I, P, P, P, P, I, I, I, I, I, ctypes.c_float,
-                                                 P, P, S, P]
+    L.mbs_gemm_a4w4_from_bf16_launch.argtypes = [I, I, P, P, P, P, P, I, I, I, I, I,
+                                                 ctypes.c_float, P, P, S, P]
     L.mbs_gemm_a4w4_from_bf16_launch.restype = I
     L.mbs_gemm_a4w4_from_bf16_workspace_bytes.argtypes = [I, I, I]
     L.mbs_gemm_a4w4_from_bf16_workspace_bytes.restype = S
@@ -245,9 +245,10 @@ def test_from_bf16_entry_validates_before_launch():
     other = [i for i, n in enumerate(names) if not n.startswith("skinny")]
     assert len(skinny) == 7 and other
     K, snp = 512, 16
-    go = lambda cfg, x, M, N=256, K=K, Mpad=None, snp=snp, alpha=1.0: L.mbs_gemm_a4w4_from_bf16_launch(
-        cfg, 0, x, FAKE, FAKE, FAKE, M, N, K, (M + 31) // 32 * 32 if Mpad is None else Mpad, snp,
-        alpha, None, None, 0, None)
+    go = lambda cfg, x, M, N=256, K=K, Mpad=None, snp=snp, alpha=1.0, bf=None, splits=0: \
+        L.mbs_gemm_a4w4_from_bf16_launch(
+            cfg, splits, x, FAKE, FAKE, bf, FAKE, M, N, K,
+            (M + 31) // 32 * 32 if Mpad is None else Mpad, snp, alpha, None, None, 0, None)
     assert go(-1, FAKE, 33) == 1 and b"M <= 32" in L.mbs_last_error()
     assert go(-1, None, 4) == 1 and b"null" in L.mbs_last_error()
     assert go(-1, FAKE + 8, 4) == 1 and b"aligned" in L.mbs_last_error()
@@ -263,6 +264,13 @@ def test_from_bf16_entry_validates_before_launch():
     m16 = [i for i in skinny if "_m16_" in names[i]]
     assert m16 and all(go(c, FAKE, 17) == 4 for c in m16)
     assert go(-1, None, 0, Mpad=0) == 0   # empty batch: nothing launched
+    # MBS activations (B factors given): M <= 8, aligned factors, 16-row
+    # decode configurations without K splits
+    assert go(-1, FAKE, 9, bf=FAKE) == 1 and b"M <= 8" in L.mbs_last_error()
+    assert go(-1, FAKE, 4, bf=FAKE + 2) == 1 and b"aligned" in L.mbs_last_error()
+    m32 = [i for i in skinny if "_m32_" in names[i]]
+    assert m32 and all(go(c, FAKE, 4, bf=FAKE) == 4 for c in m32)
+    assert all(go(c, FAKE, 4, bf=FAKE, splits=2) == 4 for c in m16)
     assert L.mbs_gemm_a4w4_from_bf16_workspace_bytes(33, 256, 512) == 0
     assert L.mbs_gemm_a4w4_from_bf16_workspace_bytes(1, 8192, 8192) == 0   # no split at this size
 

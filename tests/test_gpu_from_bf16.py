@@ -180,3 +180,75 @@ def test_large_m_and_empty(dev):
     empty = torch.empty(0, 512, dtype=torch.bfloat16, device=dev)
     say("from_bf16 M=0")
     assert mbs_amd.gemm_a4w4_from_bf16(empty, B, Bs, one_launch=True).shape == (0, 256)
+
+
+def sixteen_row_configs():
+    import mbs_amd
+
+    e = mbs_amd.ext()
+    return [c for c in range(e.num_configs()) if e.config_name(c).startswith("skinny_m16_")]
+
+
+def two_step_mbs(x, B, Bs, Bf, config=-1, alpha=1.0, bias=None):
+    """The reference's MBS decode flow: MBS-quantize the activation (factor
+    byte per row), then the factor GEMM with both factors."""
+    import mbs_amd
+
+    A, As, Af = mbs_amd.quantize_mxfp4_mbs(x)
+    if config < 0:
+        return mbs_amd.gemm_a4w4(A, B, As, Bs, Af, Bf, alpha=alpha, bias=bias)
+    return mbs_amd.ext().gemm_a4w4_config(config, 1, A, B, As, Bs, Af, Bf, alpha, bias)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 8192, 8192), (4, 8192, 8192), (8, 8192, 8192),
+                                   (3, 1280, 576), (6, 96, 64), (5, 4096, 4160)])
+def test_mbs_activation_one_launch(dev, M, N, K):
+    """With the weights' MBS factors the one-launch form MBS-quantizes the
+    activation (each workgroup derives the row factor bytes from the rows'
+    maxima over all of K) and applies both factors: equal, bit for bit, to
+    quantize_mxfp4_mbs followed by the factor GEMM on the same plan."""
+    import torch
+
+    import mbs_amd
+
+    x, B, Bs = operands(M, N, K, 300 + M * 3 + K, dev)
+    Bf = torch.randint(0, 256, (N,), dtype=torch.uint8,
+                       generator=torch.Generator().manual_seed(M + N)).to(dev)
+    for c in sixteen_row_configs():
+        say(f"from_bf16 MBS config={mbs_amd.ext().config_name(c)} M={M} N={N} K={K}")
+        got = mbs_amd.gemm_a4w4_from_bf16(x, B, Bs, config=c, B_factor=Bf)
+        same_bits(got, two_step_mbs(x, B, Bs, Bf, c), f"MBS config {c}")
+    if "splits=1" in mbs_amd.ext().plan_name(M, N, K):
+        say(f"from_bf16 MBS default plan M={M}")
+        got = mbs_amd.gemm_a4w4_from_bf16(x, B, Bs, B_factor=Bf, one_launch=True)
+        same_bits(got, two_step_mbs(x, B, Bs, Bf), "MBS default plan")
+        same_bits(mbs_amd.gemm_a4w4_from_bf16(x, B, Bs, B_factor=Bf), got, "MBS default form")
+
+
+def test_mbs_activation_specials_and_affine(dev):
+    """Rows whose maximum is zero, infinite or NaN (factor byte 0), a row of
+    tiny values (a large factor) and the affine epilogue with MBS factors."""
+    import torch
+
+    import mbs_amd
+
+    M, N, K = 8, 512, 1024
+    rng = np.random.default_rng(17)
+    bits = (rng.standard_normal((M, K)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    bits[0, :] = 0                         # all-zero row
+    bits[1, 77] = 0x7F80                   # +inf in the row
+    bits[2, 5] = 0xFFC0                    # NaN in the row
+    bits[3, :] = (bits[3, :] & 0x8000) | 0x2000   # tiny values: max far below 6
+    bits[4, 0] = 0x7F7F                    # the largest finite value
+    x = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).to(dev)
+    _, B, Bs = operands(1, N, K, 23, dev)
+    Bf = torch.randint(0, 256, (N,), dtype=torch.uint8, generator=torch.Generator().manual_seed(5)).to(dev)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(6)) * 3).to(torch.bfloat16).to(dev)
+    for c in sixteen_row_configs():
+        for alpha, b in [(1.0, None), (0.75, bias)]:
+            say(f"from_bf16 MBS specials config={mbs_amd.ext().config_name(c)} alpha={alpha}")
+            got = mbs_amd.gemm_a4w4_from_bf16(x, B, Bs, alpha=alpha, bias=b, config=c, B_factor=Bf)
+            same_bits(got, two_step_mbs(x, B, Bs, Bf, c, alpha, b), f"MBS specials config {c}")
+    with pytest.raises(RuntimeError, match="M <= 8"):
+        xs, _, _ = operands(9, N, K, 1, dev)
+        mbs_amd.gemm_a4w4_from_bf16(xs, B, Bs, B_factor=Bf, one_launch=True)
