@@ -82,17 +82,21 @@ quantize_bf16_kernel(const uint16_t* __restrict__ x, int rows, int K, uint8_t* _
 // f(b) = 1/(1 + b/256) undoes.
 // Longest row the MBS kernel keeps in LDS (64 KiB of bf16).
 constexpr int kMbsStagedK = 32768;
+// Row counts below this take 1024 threads per row.
+constexpr int kMbsWideRows = 256;
 
 // STAGED (K * 2 bytes of dynamic LDS, K <= kMbsStagedK): the first pass
 // also keeps the row in LDS and the quantize pass reads it from there, so the
 // row is read from memory once; otherwise the quantize pass reads it again.
-template <bool STAGED>
-__global__ void __launch_bounds__(256)
+// NT threads per row: 1024 for few rows (decode batches, where the row's
+// latency is the kernel's time), 256 otherwise.
+template <bool STAGED, int NT>
+__global__ void __launch_bounds__(NT)
 quantize_mbs_bf16_kernel(const uint16_t* __restrict__ x, int rows, int K, uint8_t* __restrict__ packed,
                          uint8_t* __restrict__ sshuf, uint8_t* __restrict__ splain,
                          uint8_t* __restrict__ factors, int snp, uint8_t pad)
 {
-    __shared__ uint32_t red[4];
+    __shared__ uint32_t red[NT / 64];
     extern __shared__ __attribute__((aligned(16))) uint8_t mbs_row[];
     i32x4* srow = reinterpret_cast<i32x4*>(mbs_row);
     const int r = blockIdx.x;
@@ -100,15 +104,15 @@ quantize_mbs_bf16_kernel(const uint16_t* __restrict__ x, int rows, int K, uint8_
     // a padding row's workgroup only writes its pad bytes; every row writes
     // its padding blocks [K/32, scaleN_pad).
     if (r >= rows) {
-        for (int b = threadIdx.x; b < snp; b += 256) sshuf[flat_s(r, b, snp)] = pad;
+        for (int b = threadIdx.x; b < snp; b += NT) sshuf[flat_s(r, b, snp)] = pad;
         return;
     }
     if (sshuf)
-        for (int b = (K >> 5) + threadIdx.x; b < snp; b += 256) sshuf[flat_s(r, b, snp)] = pad;
+        for (int b = (K >> 5) + threadIdx.x; b < snp; b += NT) sshuf[flat_s(r, b, snp)] = pad;
     const uint16_t* xr = x + (int64_t)r * K;
     // row maximum on the magnitude bits; a NaN maps above every number
     uint32_t amax = 0;
-    for (int e = threadIdx.x * 8; e < K; e += 256 * 8) {
+    for (int e = threadIdx.x * 8; e < K; e += NT * 8) {
         const i32x4 v = *reinterpret_cast<const i32x4*>(xr + e);
         if constexpr (STAGED) srow[e >> 3] = v;
         for (int i = 0; i < 8; ++i) {
@@ -123,17 +127,17 @@ quantize_mbs_bf16_kernel(const uint16_t* __restrict__ x, int rows, int K, uint8_
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
     __syncthreads();
     amax = red[0];
-    for (int i = 1; i < 4; ++i) amax = red[i] > amax ? red[i] : amax;
+    for (int i = 1; i < NT / 64; ++i) amax = red[i] > amax ? red[i] : amax;
     const uint32_t fb = mbs_factor_byte(amax);
     const float m = __uint_as_float(0x3F800000u | (fb << 15));
     if (threadIdx.x == 0) factors[r] = (uint8_t)fb;
     // Quantize pass, four lanes per 32-element block as in the plain kernel:
-    // quad k of the workgroup takes blocks k, k + 64, ...; lane q of the quad
+    // quad k of the workgroup takes blocks k, k + NT/4, ...; lane q of the quad
     // elements 8q..8q+7 of the block.  nb blocks per row: whole quads take
     // part in an iteration or none does, so the quad exchanges read active lanes.
     const int nb = K >> 5;
     const int q = threadIdx.x & 3;
-    for (int b = threadIdx.x >> 2; b < nb; b += 64) {
+    for (int b = threadIdx.x >> 2; b < nb; b += NT / 4) {
         i32x4 v;
         if constexpr (STAGED) v = srow[(b * 32 + q * 8) >> 3];   // written before the barrier above
         else v = *reinterpret_cast<const i32x4*>(xr + b * 32 + q * 8);
@@ -350,14 +354,25 @@ int mbs_quantize_mxfp4_mbs_bf16(const void* x, int rows, int K, uint8_t* packed,
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int snp = scale_pad_of(K);
     const int grid = scale_shuffled ? ((rows + 31) & ~31) : rows;  // padding rows included
-    if (K <= kMbsStagedK)
-        hipLaunchKernelGGL(quantize_mbs_bf16_kernel<true>, dim3(grid), dim3(256), (size_t)K * 2, s,
-                           static_cast<const uint16_t*>(x), rows, K, packed, scale_shuffled,
-                           scale_plain, factors, snp, (uint8_t)pad_byte);
-    else
-        hipLaunchKernelGGL(quantize_mbs_bf16_kernel<false>, dim3(grid), dim3(256), 0, s,
-                           static_cast<const uint16_t*>(x), rows, K, packed, scale_shuffled,
-                           scale_plain, factors, snp, (uint8_t)pad_byte);
+    const auto* xs = static_cast<const uint16_t*>(x);
+    const uint8_t pb = (uint8_t)pad_byte;
+    // Fewer rows than CUs: a row's latency is the kernel's time, so give each
+    // row four times the threads.
+    const bool wide = rows < kMbsWideRows;
+    if (K <= kMbsStagedK) {
+        if (wide)
+            hipLaunchKernelGGL((quantize_mbs_bf16_kernel<true, 1024>), dim3(grid), dim3(1024), (size_t)K * 2,
+                               s, xs, rows, K, packed, scale_shuffled, scale_plain, factors, snp, pb);
+        else
+            hipLaunchKernelGGL((quantize_mbs_bf16_kernel<true, 256>), dim3(grid), dim3(256), (size_t)K * 2,
+                               s, xs, rows, K, packed, scale_shuffled, scale_plain, factors, snp, pb);
+    } else if (wide) {
+        hipLaunchKernelGGL((quantize_mbs_bf16_kernel<false, 1024>), dim3(grid), dim3(1024), 0, s, xs,
+                           rows, K, packed, scale_shuffled, scale_plain, factors, snp, pb);
+    } else {
+        hipLaunchKernelGGL((quantize_mbs_bf16_kernel<false, 256>), dim3(grid), dim3(256), 0, s, xs,
+                           rows, K, packed, scale_shuffled, scale_plain, factors, snp, pb);
+    }
     return launched();
 }
 

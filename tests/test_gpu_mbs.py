@@ -44,9 +44,10 @@ def run_gpu_mbs(bits):
 
 
 # K = 32768 is the longest row the kernel stages in LDS; K = 32800 takes the
-# two-pass (unstaged) form.
+# two-pass (unstaged) form.  Fewer than 256 rows run 1024 threads per row,
+# more run 256 (the last two shapes).
 @pytest.mark.parametrize("R,K", [(1, 32), (7, 64), (33, 256), (64, 8192), (3, 12288), (7, 32768),
-                                 (7, 32800)])
+                                 (7, 32800), (300, 1024), (257, 32800)])
 def test_mbs_quantizer_bit_exact(dev, R, K):
     rng = np.random.default_rng(R * 131 + K)
     bits = bf16_rows(rng, R, K)
