@@ -208,7 +208,9 @@ int mbs_gemm_a4w4_launch_config(int config, int splits, const uint8_t* A, const 
  * reference has no fused form.  Every workgroup quantizes the rows it needs
  * itself: for M <= 8 (only the live rows' blocks) this is faster than the two
  * launches; for larger M each workgroup re-quantizes 16 or 32 rows and the
- * two launches are faster (measured at N = K = 8192 on MI355X). */
+ * two launches are faster (measured at N = K = 8192 on MI355X).  With MBS
+ * activations every workgroup also reads its rows over all of K for their
+ * maxima first; one launch is then faster for M <= 4. */
 int mbs_gemm_a4w4_from_bf16_launch(int config, int splits, const void* x, const uint8_t* B,
                                    const uint8_t* BScale, const uint8_t* BFactor, void* out, int M,
                                    int N, int K, int Mpad, int scaleN_pad, float alpha,
