@@ -430,9 +430,9 @@ at::Tensor gemm_a4w4_grouped(at::Tensor A, at::Tensor B, at::Tensor A_scale, at:
 // rows of A: at M = 16 / 32 one launch takes longer than two).  config/splits
 // force a skinny configuration (one launch only; -1: the heuristic's).
 // With MBS activations every workgroup first takes the rows' maxima over all
-// of K: one launch for M <= 4 (9.7 / 10.6 us against 10.8 / 11.1 us for
+// of K: one launch for M <= 4 (9.8 / 10.3 us against 10.8 / 11.1 us for
 // quantize_mxfp4_mbs + the factor GEMM at M = 1 / 4), two launches above
-// (14.4 against 11.4 us at M = 8).
+// (13.5 against 11.5 us at M = 8).
 constexpr int64_t kOneLaunchMaxM = 8;
 constexpr int64_t kOneLaunchMaxMbsM = 4;
 

@@ -1553,23 +1553,61 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
         static_for<MT>([&](auto m) { acc[f][m] = f32x4{0.f, 0.f, 0.f, 0.f}; });
     });
 
+    // Scale dwords and B fragments of the batch starting at stage st.
+    auto issue_b = [&](int st, i32x4 (&b)[UB][NF], int (&sb)[UB / 2][NG]) {
+        static_for<UB / 2>([&](auto v) {
+            const int g = (st >> 1) + v;
+            const bool ok = st + 2 * v < my_end;
+            static_for<NG>([&](auto G) {
+                sb[v][G] = load4(rBs, ok ? (uint32_t)(G * 32 * p.snp + g * 256 + lane * 4) : kOOB);
+            });
+        });
+        static_for<UB>([&](auto u) {
+            const int s = st + u;
+            const bool zap = (ktail && s == S_total - 1 && hi_lane) || s >= my_end;
+            static_for<NF>([&](auto f) {
+                b[u][f] = load16nt(rB, zap ? kOOB : (uint32_t)(f * fstride + s * 1024 + lane * 16));
+            });
+        });
+    };
     float mrow[NP];   // XMBS: the multiplier 1 + b/256 of each pass's row
+    // XMBS, one pass: the first PA chunks of every row go out first, then the
+    // first batch's B; the row maxima wait for those chunks only (loads
+    // return in issue order), and the barriers wait for LDS only, so the B
+    // batch streams during the maximum pass.
+    constexpr bool PRE_B = XMBS && NP == 1;
+    constexpr int PA = 2;
+    i32x4 b_first[PRE_B ? UB : 1][NF];
+    int sb_first[PRE_B ? UB / 2 : 1][NG];
     if constexpr (XMBS) {
-        for (int r = 0; r < 4 * NP; ++r) {   // rows >= M read zeros
+        constexpr int NR = 4 * NP;   // rows >= M read zeros
+        const int e0 = (kw * 64 + lane) * 8;
+        i32x4 a0[NR][PA];
+        static_for<NR>([&](auto r) {
+            static_for<PA>([&](auto j) {
+                const int e = e0 + j * NWK * 512;
+                a0[r][j] = load16(rA, e < K ? (uint32_t)((r * K + e) * 2) : kOOB);
+            });
+        });
+        if constexpr (PRE_B) issue_b(my_begin, b_first, sb_first);
+        static_for<NR>([&](auto r) {
             uint32_t amax = 0;
-            for (int e = (kw * 64 + lane) * 8; e < K; e += NWK * 64 * 8)
+            static_for<PA>([&](auto j) { amax = max(amax, bf16x8_absmax(a0[r][j])); });
+            for (int e = e0 + PA * NWK * 512; e < K; e += NWK * 512)
                 amax = max(amax, bf16x8_absmax(load16(rA, (uint32_t)((r * K + e) * 2))));
             for (int off = 32; off >= 1; off >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, off));
             if (lane == 0) row_max[kw][r] = amax;
-        }
-        __syncthreads();
+        });
+        wait_lgkmcnt0();
+        barrier();
         if (threadIdx.x < 16) {
             uint32_t amax = 0;
-            if (threadIdx.x < 4 * NP)
+            if (threadIdx.x < NR)
                 for (int k = 0; k < NWK; ++k) amax = max(amax, row_max[k][threadIdx.x]);
             row_fb[threadIdx.x] = mbs_factor_byte(amax);
         }
-        __syncthreads();
+        wait_lgkmcnt0();
+        barrier();
         static_for<NP>([&](auto q) {
             mrow[q] = __uint_as_float(0x3F800000u | (row_fb[4 * q + (lane >> 4)] << 15));
         });
@@ -1594,35 +1632,44 @@ __global__ void __launch_bounds__(64 * NWK) gemm_skinny_kernel(const GemmArgs p)
         // Scales first: loads return in issue order, so stage u's MFMAs then
         // wait only for stage u's B and A, and the MFMAs trail the stream
         // instead of starting after the whole batch has landed.
-        static_for<UB / 2>([&](auto v) {
-            const int g = (st >> 1) + v;
-            const bool ok = st + 2 * v < my_end;
-            static_for<NG>([&](auto G) {
-                sb[v][G] = load4(rBs, ok ? (uint32_t)(G * 32 * p.snp + g * 256 + lane * 4) : kOOB);
+        if constexpr (PRE_B) {
+            if (st == my_begin) {
+                static_for<UB>([&](auto u) { static_for<NF>([&](auto f) { b[u][f] = b_first[u][f]; }); });
+                static_for<UB / 2>([&](auto v) { static_for<NG>([&](auto G) { sb[v][G] = sb_first[v][G]; }); });
+            } else {
+                issue_b(st, b, sb);
+            }
+        } else {
+            static_for<UB / 2>([&](auto v) {
+                const int g = (st >> 1) + v;
+                const bool ok = st + 2 * v < my_end;
+                static_for<NG>([&](auto G) {
+                    sb[v][G] = load4(rBs, ok ? (uint32_t)(G * 32 * p.snp + g * 256 + lane * 4) : kOOB);
+                });
+                if constexpr (!XBF) sa[v] = load4(rAs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
             });
-            if constexpr (!XBF) sa[v] = load4(rAs, ok ? (uint32_t)(g * 256 + lane * 4) : kOOB);
-        });
-        static_for<UB>([&](auto u) {
-            const int s = st + u;
-            const bool ok = s < my_end;
-            const bool zap = (ktail && s == S_total - 1 && hi_lane) || !ok;
-            static_for<NF>([&](auto f) {
-                b[u][f] = load16nt(rB, zap ? kOOB : (uint32_t)(f * fstride + s * 1024 + lane * 16));
+            static_for<UB>([&](auto u) {
+                const int s = st + u;
+                const bool ok = s < my_end;
+                const bool zap = (ktail && s == S_total - 1 && hi_lane) || !ok;
+                static_for<NF>([&](auto f) {
+                    b[u][f] = load16nt(rB, zap ? kOOB : (uint32_t)(f * fstride + s * 1024 + lane * 16));
+                });
+                static_for<MT>([&](auto m) {
+                    if constexpr (XC) {
+                    } else if constexpr (XBF) {
+                        // a row tile wholly past M reads nothing (and is not quantized)
+                        const bool dead = zap || 16 * m >= p.M;
+                        const uint32_t o = (uint32_t)(((16 * m + (lane & 15)) * K + s * 128 + (lane >> 4) * 32) * 2);
+                        static_for<4>([&](auto i) { x[u][m][i] = load16(rA, dead ? kOOB : o + 16 * i); });
+                    } else {
+                        a[u][m] = load16(rA, zap ? kOOB
+                                                 : (uint32_t)((16 * m + (lane & 15)) * Kp + s * 64 +
+                                                              (lane >> 4) * 16));
+                    }
+                });
             });
-            static_for<MT>([&](auto m) {
-                if constexpr (XC) {
-                } else if constexpr (XBF) {
-                    // a row tile wholly past M reads nothing (and is not quantized)
-                    const bool dead = zap || 16 * m >= p.M;
-                    const uint32_t o = (uint32_t)(((16 * m + (lane & 15)) * K + s * 128 + (lane >> 4) * 32) * 2);
-                    static_for<4>([&](auto i) { x[u][m][i] = load16(rA, dead ? kOOB : o + 16 * i); });
-                } else {
-                    a[u][m] = load16(rA, zap ? kOOB
-                                             : (uint32_t)((16 * m + (lane & 15)) * Kp + s * 64 +
-                                                          (lane >> 4) * 16));
-                }
-            });
-        });
+        }
         // Every load of the batch is issued before the first MFMA; left to
         // itself the scheduler interleaves them with the MFMAs and the wave
         // keeps only a fraction of its batch in flight.
